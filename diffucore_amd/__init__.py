@@ -1,0 +1,16 @@
+"""diffucore_amd: diffucore's quantized denoiser hot path (INT8 flash attention
+and W8A8 linears) as hand-written gfx950 (MI355X) HIP kernels behind a C ABI,
+with the reference's Python operator surface on top."""
+
+from ._attention import (attention_bhld, attention_blhd, fa2_turing_available, int8_attention,
+                         int8_turing_available, resolve_attention_backend, set_attention_backend)
+from ._int8 import (GROUP, Int8Linear, dequantize_linears, dequantize_weight, int8_fast_available, int8_mlp,
+                    int_mm, quantize_activation, quantize_linears, quantize_weight, rescale, scaled_mm)
+from .runtime import DevicePolicy
+
+__all__ = [
+    "GROUP", "DevicePolicy", "Int8Linear", "attention_bhld", "attention_blhd", "dequantize_linears",
+    "dequantize_weight", "fa2_turing_available", "int8_attention", "int8_fast_available", "int8_mlp",
+    "int8_turing_available", "int_mm", "quantize_activation", "quantize_linears", "quantize_weight",
+    "rescale", "resolve_attention_backend", "scaled_mm", "set_attention_backend",
+]

@@ -1,0 +1,54 @@
+"""Build ``libdiffucore_amd.so`` (the gfx950 kernels behind the C ABI in
+``include/diffucore_amd.h``) in-tree with hipcc.
+
+Run ``python -m diffucore_amd.build``. The library sits next to this file so it
+travels with the source tree; it is loaded by :mod:`diffucore_amd._lib`.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libdiffucore_amd.so"
+SOURCES = ["quant.hip", "gemm.hip", "attn.hip", "capi.cpp"]
+ARCH = "gfx950"
+
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-shared", "-fPIC",
+    # reproducible float32 arithmetic: only explicit fmaf() contracts
+    "-ffp-contract=off",
+    # no packed-fp32 VALU instructions
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (needs ROCm)")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into ``LIB`` (always recompiles)."""
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *FLAGS, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES]]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    out = build(verbose="-v" in sys.argv)
+    print(f"built {out}")

@@ -1,0 +1,118 @@
+/*
+ * diffucore_amd: C ABI of the MI355X (gfx950) quantized denoiser hot path.
+ *
+ * The reference (nawka12/diffucore) binds this path from Python: Triton
+ * kernels and torch ops in src/diffucore/models/_int8.py, and two pybind11
+ * extension modules built by torch.utils.cpp_extension,
+ * src/diffucore/kernels/int8_attn_sm80.cu (fwd) and
+ * src/diffucore/kernels/int8_gemm_sm75.cu (scaled_mm). Each entry point below
+ * names the reference interface it replaces.
+ *
+ * Conventions (all entry points):
+ *  - Plain C types only. Device pointers are raw HIP device addresses.
+ *  - `stream` is a hipStream_t (NULL = the null stream). Every entry point only
+ *    enqueues work on `stream`; none synchronizes and none allocates memory.
+ *  - Return 0 on success, else one of DC_E*; dc_last_error() then holds a
+ *    thread-local message.
+ *  - dtype codes: DC_F16, DC_BF16, DC_F32, DC_I32 (GEMM output only).
+ *  - Work runs on the calling thread's current HIP device.
+ */
+#ifndef DIFFUCORE_AMD_H
+#define DIFFUCORE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { DC_F16 = 0, DC_BF16 = 1, DC_F32 = 2, DC_I32 = 3, DC_NONE = -1 };
+enum { DC_OK = 0, DC_EINVAL = 1, DC_EUNSUPPORTED = 2, DC_EHIP = 3, DC_EWORKSPACE = 4 };
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* dc_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int dc_abi_version(void);
+
+/*
+ * Per-row int8 activation quantization, optionally after the ConvRot rotation.
+ * Replaces quantize_activation (src/diffucore/models/_int8.py:299-310), i.e.
+ * the Triton _rot_quant_kernel (_int8.py:399-406) and its torch fallback
+ * _quantize_rows(_rotate(x.float(), group)) (_int8.py:87-97, 79-84).
+ *
+ *   x      [M, K] of x_dtype (DC_F16/DC_BF16/DC_F32), row stride ldx elements
+ *   group  0 (none) or 256 (x @ H_256 per 256-wide group; needs K % 256 == 0)
+ *   q      [M, K] int8 out, row stride ldq bytes
+ *   scale  [M] float32 out: max(amax / 127, 1e-30)
+ * Codes are clamp(rint(x / scale), -128, 127) with an IEEE float32 division.
+ */
+int dc_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int group,
+                     int8_t* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * W8A8 GEMM on int8 MFMA with int32 accumulation and a fused epilogue.
+ *   a   [M, K] int8 (activations), row stride lda
+ *   w   [N, K] int8 (nn.Linear weight layout), row stride ldw
+ * out_dtype == DC_I32: out = a @ w.T as int32 (sx, sw, bias ignored).
+ *   Replaces int_mm (src/diffucore/models/_int8.py:200-207), torch._int_mm.
+ * out_dtype in {DC_F16, DC_BF16, DC_F32}:
+ *   out[m, n] = cast(float(acc[m, n]) * (sx[m] * sw[n])), then, when bias is
+ *   given (bias_dtype != DC_NONE), out = cast(out + cast(bias[n])).
+ *   Replaces scaled_mm (_int8.py:266-276; kernels/int8_gemm_sm75.cu:75-88)
+ *   and int_mm + rescale (_int8.py:313-323), rounding bit for bit like them.
+ * Needs K % 16 == 0, lda % 16 == 0, ldw % 16 == 0 and 16-byte aligned a, w.
+ */
+int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, const float* sx,
+                 const float* sw, const void* bias, int bias_dtype, void* out, int out_dtype,
+                 int64_t ldo, int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * The rescale pass on an int32 accumulator, for callers that hold one.
+ * Replaces rescale (src/diffucore/models/_int8.py:313-323) and the Triton
+ * _rescale_kernel (_int8.py:408-417). Same rounding as dc_w8a8_gemm.
+ */
+int dc_rescale(const int32_t* acc, int64_t lda, const float* sx, const float* sw,
+               const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
+               int64_t M, int64_t N, void* stream);
+
+/*
+ * Workspace size in bytes for dc_int8_attn_fwd at this shape.
+ * Replaces the scratch tensors fwd allocates itself
+ * (src/diffucore/kernels/int8_attn_sm80.cu:469-476).
+ */
+size_t dc_int8_attn_workspace_bytes(int B, int H, int Lq, int Lk, int D);
+
+/*
+ * INT8-QK / 16-bit-PV flash attention.
+ * Replaces fwd(q, k, v, sm_scale) (src/diffucore/kernels/int8_attn_sm80.cu:460-497),
+ * called from attention_blhd / attention_bhld (src/diffucore/models/_attention.py:216-217, 268-271).
+ *   q [B, Lq, H, D], k and v [B, Lk, H, D], o [B, Lq, H, D], all of `dtype`
+ *   (DC_F16 or DC_BF16), given as element strides for the (B, L, H) dims;
+ *   D is contiguous. D % 8 == 0, D <= 128, strides % 8 == 0, 16-byte aligned.
+ *   sm_scale: softmax scale (the reference passes D ** -0.5).
+ * K is smoothed by its per-channel mean and quantized per 64-key block; Q is
+ * quantized per token; S = Q K^T runs on int8 MFMA into int32; the online
+ * softmax is float32 in base 2; P V runs on 16-bit MFMA with float32
+ * accumulation. The workspace (dc_int8_attn_workspace_bytes) holds, at
+ * 256-byte aligned offsets in this order:
+ *   q8  int8 [B, H, Lq128, Dp]   Lq128 = Lq rounded up to 128, Dp = 64 or 128
+ *   qs  f32  [B, H, Lq128]       per-token scale amax / 127
+ *   k8  int8 [B, H, Lk64, Dp]    Lk64 = Lk rounded up to 64
+ *   ks  f32  [B, H, Lk64 / 64]   per-block scale amax / 127
+ *   vt  16-bit [B, H, Dp, Lk64]  V transposed (MFMA operand order)
+ *   kpart f32 [B, H, ceil(Lk / 128), D]   per-window key sums
+ *   ksum  f32 [B, H, D]                    per-channel key sums
+ */
+int dc_int8_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                     int H, int Lq, int Lk, int D, const int64_t q_strides[3],
+                     const int64_t k_strides[3], const int64_t v_strides[3],
+                     const int64_t o_strides[3], float sm_scale, void* workspace,
+                     size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DIFFUCORE_AMD_H */

@@ -1,0 +1,99 @@
+"""Oracle: per-row int8 quantizer and ConvRot rotation (test infrastructure only).
+
+Follows reference ``src/diffucore/models/_int8.py``:
+
+* ``quantize_rows``  <- ``_quantize_rows`` (``_int8.py:87-97``) and the Triton
+  ``_store_quantized`` (``_int8.py:392-397``): ``scale = max(amax/127, 1e-30)``,
+  ``q = clamp(rint(x / scale), -128, 127)``, all in float32 with an IEEE
+  division.
+* ``hadamard``       <- ``_hadamard`` (``_int8.py:64-76``).
+* ``rotate_matmul``  <- ``_rotate`` (``_int8.py:79-84``): ``t @ H`` per group.
+* ``rotate_butterfly`` <- ``_hadamard_rows`` (``_int8.py:363-372``), with the
+  summation order this build fixes (see its docstring).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+_H4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], np.float32)
+SCALE_FLOOR = np.float32(1e-30)
+
+
+def quantize_rows(t) -> tuple[np.ndarray, np.ndarray]:
+    """(int8 [M, K], float32 scale [M]) for float32 rows ``t`` [M, K]."""
+    t = np.asarray(t, np.float32)
+    amax = np.abs(t).max(axis=-1) if t.shape[-1] else np.zeros(t.shape[:-1], np.float32)
+    scale = np.maximum(amax / np.float32(127.0), SCALE_FLOOR).astype(np.float32)
+    x = (t / scale[..., None]).astype(np.float32)
+    q = np.clip(np.rint(x), -128, 127).astype(np.int8)
+    return q, scale
+
+
+def hadamard(n: int) -> np.ndarray:
+    """Normalized regular Hadamard of order ``n`` (a power of 4), float32."""
+    h = _H4
+    while h.shape[0] < n:
+        h = np.kron(h, _H4)
+    if h.shape[0] != n:
+        raise ValueError(f"ConvRot group must be a power of 4, got {n}")
+    return (h / np.float32(n ** 0.5)).astype(np.float32)
+
+
+def rotate_matmul(t, group: int) -> np.ndarray:
+    """``t @ H`` per ``group``-wide slice of the last dim (float32 matmul)."""
+    t = np.asarray(t, np.float32)
+    if not group:
+        return t
+    shape = t.shape
+    out = t.reshape(-1, shape[-1] // group, group) @ hadamard(group)
+    return out.reshape(shape).astype(np.float32)
+
+
+def _h4_along(y: np.ndarray, axis: int) -> np.ndarray:
+    """``y @ H4`` along ``axis`` (length 4): ``S - 2 * y[3 - j]`` with the sum
+    formed pairwise, ``S = (y0 + y1) + (y2 + y3)``."""
+    y0, y1, y2, y3 = (np.take(y, i, axis=axis) for i in range(4))
+    s = (y0 + y1) + (y2 + y3)
+    out = [s - np.float32(2.0) * yy for yy in (y3, y2, y1, y0)]
+    return np.stack(out, axis=axis).astype(np.float32)
+
+
+def rotate_butterfly(t, group: int = 256) -> np.ndarray:
+    """ConvRot rotation as the in-register butterfly the HIP kernel runs.
+
+    The in-group index ``i`` (0..255) is read as four base-4 digits
+    ``i = 64*d1 + 16*d2 + 4*d3 + d4``; ``H4`` is applied along ``d1``, then
+    ``d2``, ``d3``, ``d4`` (the reference's Triton order, ``_int8.py:367-371``),
+    each as ``sum - 2 * reversed`` with the four-term sum taken pairwise
+    ``(y0 + y1) + (y2 + y3)``; the result is scaled by 1/16 last (exact).
+    The reference's Triton ``tl.sum`` order is implementation-defined, so this
+    pairwise order is the one this build documents and pins.
+    """
+    t = np.asarray(t, np.float32)
+    if not group:
+        return t
+    if group != 256:
+        raise ValueError("the butterfly is defined for group 256")
+    shape = t.shape
+    y = t.reshape(-1, shape[-1] // 256, 4, 4, 4, 4)
+    for axis in (2, 3, 4, 5):
+        y = _h4_along(y, axis)
+    return (y.reshape(shape) * np.float32(0.0625)).astype(np.float32)
+
+
+def quantize_activation(x, group: int) -> tuple[np.ndarray, np.ndarray]:
+    """What the HIP quantize kernel computes: butterfly rotation (group 256)
+    or none (group 0), then ``quantize_rows``."""
+    x = np.asarray(x, np.float32)
+    return quantize_rows(rotate_butterfly(x, group) if group else x)
+
+
+def quantize_weight(w, group: int) -> tuple[np.ndarray, np.ndarray]:
+    """``quantize_weight`` (``_int8.py:100-102``): matmul-form rotation."""
+    return quantize_rows(rotate_matmul(np.asarray(w, np.float32), group))
+
+
+def dequantize_weight(q, scale, group: int) -> np.ndarray:
+    """``dequantize_weight`` (``_int8.py:105-107``)."""
+    return rotate_matmul(np.asarray(q, np.float32) * np.asarray(scale, np.float32)[:, None], group)

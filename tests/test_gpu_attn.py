@@ -1,0 +1,136 @@
+"""dc_int8_attn_fwd on the GPU.
+
+* K smoothing / quantization and Q quantization: bit-exact against the oracle
+  (reference ``int8_attn_sm80.cu:38-142, 341-388``), read back from the
+  documented workspace.
+* Output: against the oracle's restatement of the algorithm (tight bound) and
+  against float32 SDPA with the reference's own bar, rel L2 < 3e-2 and
+  cosine > 0.9995 (``tests/test_attention_dispatch.py:198-213``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from diffucore_amd import _attention as A
+from oracle import attn as OA
+from tests._util import DT, cosine, max_abs, np32, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+# tolerance against the oracle's restatement (same quantization, exact softmax):
+# the output itself is rounded to the 16-bit type on both sides, so the bound
+# scales with that type's precision (bf16 ulp 2^-8, fp16 ulp 2^-11)
+ORACLE_REL = {torch.float16: 1e-3, torch.bfloat16: 4e-3}
+ORACLE_COS = 0.99999
+
+
+def _ref_blhd(q, k, v):
+    out = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    return out.transpose(1, 2)
+
+
+def _inputs(B, Lq, Lk, H, D, dtype, seed=0, k_offset=0.5):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Lq, H, D, generator=g)
+    k = torch.randn(B, Lk, H, D, generator=g) + k_offset
+    v = torch.randn(B, Lk, H, D, generator=g)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def _run(q, k, v, gpu):
+    B, Lq, H, D = q.shape
+    Lk = k.shape[1]
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    ws = torch.empty(A.workspace_bytes(B, H, Lq, Lk, D), device=gpu, dtype=torch.uint8)
+    out = A.int8_attention(qd, kd, vd, D ** -0.5, workspace=ws)
+    return out, A.workspace_views(ws, B, H, Lq, Lk, D)
+
+
+CASES = [
+    # the reference's own shapes (tests/test_attention_dispatch.py:199-200), head dim 128
+    (1, 1024, 1024, 4, 128, torch.float16), (2, 1000, 1000, 2, 128, torch.float16),
+    (1, 700, 77, 4, 128, torch.float16), (1, 70, 3953, 2, 128, torch.float16),
+    # extensions: bf16 (FLUX), head dim 64 (SDXL), 40 (SD1.5, padded to 64)
+    (1, 1024, 1024, 4, 128, torch.bfloat16), (2, 300, 500, 3, 64, torch.float16),
+    (2, 257, 77, 2, 40, torch.float16), (1, 333, 190, 2, 40, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("B,Lq,Lk,H,D,dtype", CASES)
+def test_codes_and_scales_bit_exact(gpu, B, Lq, Lk, H, D, dtype):
+    q, k, v = _inputs(B, Lq, Lk, H, D, dtype)
+    _, ws = _run(q, k, v, gpu)
+    ksum = OA.k_colsum(np32(k))
+    assert np.array_equal(ws["ksum"].cpu().numpy().view(np.uint32), ksum.view(np.uint32))
+    ki, ks = OA.k_quantize(np32(k), ksum)
+    assert np.array_equal(ws["ks"].cpu().numpy().view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(ws["k8"][..., :D].cpu().numpy(), ki)
+    assert not ws["k8"][..., D:].any()
+    q8, qs = OA.q_quantize(np32(q))
+    assert np.array_equal(ws["q8"][:, :, :Lq, :D].cpu().numpy(), q8)
+    assert np.array_equal(ws["qs"][:, :, :Lq].cpu().numpy().view(np.uint32), qs.view(np.uint32))
+
+
+@pytest.mark.parametrize("B,Lq,Lk,H,D,dtype", CASES)
+def test_output_close_to_oracle_and_sdpa(gpu, B, Lq, Lk, H, D, dtype):
+    q, k, v = _inputs(B, Lq, Lk, H, D, dtype)
+    out, _ = _run(q, k, v, gpu)
+    assert out.shape == (B, Lq, H, D) and out.dtype == dtype
+    o = np32(out)
+    assert np.isfinite(o).all()
+    ora = OA.int8_attention(np32(q), np32(k), np32(v), D ** -0.5, DT[dtype], DT[dtype])
+    r, c = rel_l2(o, ora), cosine(o, ora)
+    print(f"[attn] {B},{Lq},{Lk},{H},{D},{DT[dtype]}: vs oracle rel {r:.2e} cos {c:.7f} maxabs {max_abs(o, ora):.2e}")
+    assert r < ORACLE_REL[dtype] and c > ORACLE_COS
+    ref = np32(_ref_blhd(q.float(), k.float(), v.float()))
+    r, c = rel_l2(o, ref), cosine(o, ref)
+    print(f"[attn]   vs fp32 SDPA rel {r:.2e} cos {c:.7f}")
+    assert r < 3e-2 and c > 0.9995
+
+
+def test_bhld_and_strided_inputs(gpu):
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 3, 600, 128, device=gpu).half() for _ in range(3))
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(1, 600, -1)
+    assert rel_l2(np32(A.attention_bhld(q, k, v, "int8_turing")), np32(ref)) < 3e-2
+    qkv = torch.randn(1, 500, 2, 3 * 128, device=gpu).half()   # packed: stride(2) = 384
+    q, k, v = qkv[..., :128], qkv[..., 128:256], qkv[..., 256:]
+    ref = _ref_blhd(q.float(), k.float(), v.float()).reshape(1, 500, -1)
+    out = A.attention_blhd(q, k, v, "int8_turing")
+    assert rel_l2(np32(out), np32(ref)) < 3e-2
+
+
+def test_flat_scores_large_v(gpu):
+    """Every p = 1 with large same-sign V (tests/test_attention_dispatch.py:229-238)."""
+    q = torch.zeros(1, 256, 2, 128, device=gpu).half()
+    k = torch.randn(1, 1024, 2, 128, device=gpu).half()
+    v = (torch.rand(1, 1024, 2, 128, device=gpu) * 200 + 900).half()
+    out = A.attention_blhd(q, k, v, "int8_turing")
+    assert torch.isfinite(out).all()
+    assert rel_l2(np32(out), np32(_ref_blhd(q.float(), k.float(), v.float()).reshape(1, 256, -1))) < 1e-3
+
+
+def test_zero_query_is_mean_of_v(gpu):
+    q = torch.zeros(1, 64, 1, 64, device=gpu, dtype=torch.bfloat16)
+    k = torch.randn(1, 300, 1, 64, device=gpu, dtype=torch.bfloat16)
+    v = torch.randn(1, 300, 1, 64, device=gpu, dtype=torch.bfloat16)
+    out = A.attention_blhd(q, k, v, "int8_turing")
+    mean = v.float().mean(1, keepdim=True).expand(1, 64, 1, 64).reshape(1, 64, -1)
+    assert max_abs(np32(out), np32(mean)) < 1e-2
+
+
+def test_other_head_dims_fall_back_to_sdpa(gpu):
+    torch.manual_seed(0)
+    for D in (36, 256):
+        q = torch.randn(1, 256, 2, D, device=gpu).half()
+        assert torch.equal(A.attention_blhd(q, q, q, "int8_turing"), A.attention_blhd(q, q, q, "sdpa"))
+
+
+def test_deterministic(gpu):
+    q, k, v = _inputs(1, 500, 700, 3, 128, torch.bfloat16, seed=3)
+    outs = [_run(q, k, v, gpu)[0] for _ in range(3)]
+    assert all(torch.equal(outs[0], o) for o in outs[1:])

@@ -1,0 +1,87 @@
+"""dc_w8a8_gemm / dc_rescale on the GPU against the oracle: the int32 GEMM is
+exact and the fused epilogue rounds bit for bit like ``rescale(int_mm())``
+(reference ``_int8.py:200-207, 313-323``; ``tests/test_int8.py:174-183``)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from diffucore_amd import _int8
+from oracle import gemm as OG
+from oracle import quant as OQ
+from tests._util import DT, np32, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+REF_SHAPES = [(33, 2048, 1024), (300, 512, 768), (4096, 2048, 2048), (1000, 8192, 2048)]
+EDGE_SHAPES = [(1, 64, 16), (17, 37, 48), (129, 200, 336), (512, 3072, 3072)]
+
+
+def _qw(m, n, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    sx = torch.rand(m, generator=g) * 1e-2
+    sw = torch.rand(n, generator=g) * 1e-3
+    return q, w, sx, sw
+
+
+@pytest.mark.parametrize("m,n,k", REF_SHAPES + EDGE_SHAPES)
+def test_int_mm_exact(gpu, m, n, k):
+    q, w, _, _ = _qw(m, n, k, 6)
+    acc = _int8.int_mm(q.to(gpu), w.to(gpu))
+    assert acc.dtype == torch.int32
+    assert np.array_equal(acc.cpu().numpy(), OG.int_mm(q.numpy(), w.numpy()))
+
+
+@pytest.mark.parametrize("m,n,k", REF_SHAPES + EDGE_SHAPES)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_fused_epilogue_bit_exact(gpu, m, n, k, dtype):
+    q, w, sx, sw = _qw(m, n, k, 7)
+    out = _int8.scaled_mm(q.to(gpu), w.to(gpu), sx.to(gpu), sw.to(gpu), dtype)
+    ref = OG.rescale(OG.int_mm(q.numpy(), w.numpy()), sx.numpy(), sw.numpy(), None, DT[dtype])
+    assert out.dtype == dtype
+    assert np.array_equal(np32(out).view(np.uint32), ref.view(np.uint32))
+    # the reference's own contract: fused == rescale(int_mm())
+    two = _int8.rescale(_int8.int_mm(q.to(gpu), w.to(gpu)), sx.to(gpu), sw.to(gpu), None, dtype)
+    assert torch.equal(out, two)
+
+
+@pytest.mark.parametrize("dtype,bias_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32),
+                                              (torch.float32, torch.float32), (torch.bfloat16, torch.float32)])
+def test_bias_double_rounding(gpu, dtype, bias_dtype):
+    q, w, sx, sw = _qw(300, 520, 768, 8)
+    bias = (torch.randn(520) * 0.5).to(bias_dtype)
+    lin = _int8.Int8Linear(768, 520, bias=True, group=0, device=gpu)
+    lin.weight.copy_(w.to(gpu))
+    lin.scale_bits.copy_(sw.to(gpu).view(torch.int32))
+    lin.bias = nn.Parameter(bias.to(gpu), requires_grad=False)
+    out = lin.matmul_quantized(q.to(gpu), sx.to(gpu), dtype)
+    ref = OG.rescale(OG.int_mm(q.numpy(), w.numpy()), sx.numpy(), sw.numpy(), np32(bias), DT[dtype])
+    assert np.array_equal(np32(out).view(np.uint32), ref.view(np.uint32))
+    two = _int8.rescale(_int8.int_mm(q.to(gpu), w.to(gpu)), sx.to(gpu), sw.to(gpu), bias.to(gpu), dtype)
+    assert torch.equal(out, two)
+
+
+@pytest.mark.parametrize("k,n,group", [(2048, 2048, 256), (768, 512, 256), (1024, 8192, 256), (320, 1280, 0)])
+def test_int8_linear_matches_oracle_and_float(gpu, k, n, group):
+    torch.manual_seed(4)
+    lin = nn.Linear(k, n, bias=n == 512).to(gpu).half()
+    m = _int8.Int8Linear.from_linear(lin, group)
+    x = torch.randn(3, 333, k, device=gpu, dtype=torch.float16)
+    y = m(x)
+    assert y.dtype == torch.float16 and y.shape == (3, 333, n)
+    qa, sa = OQ.quantize_activation(np32(x).reshape(-1, k), group)
+    bias = np32(m.bias) if m.bias is not None else None
+    ref = OG.w8a8_linear(qa, sa, m.weight.cpu().numpy(), m.scale.cpu().numpy(), bias, "f16")
+    assert np.array_equal(np32(y).reshape(-1, n).view(np.uint32), ref.view(np.uint32))
+    assert rel_l2(np32(y), np32(lin(x))) < 0.02
+
+
+def test_short_input(gpu):
+    lin = nn.Linear(256, 64, bias=False).to(gpu)
+    x = torch.randn(3, 256, device=gpu)
+    assert rel_l2(np32(_int8.Int8Linear.from_linear(lin)(x)), np32(lin(x))) < 0.02
