@@ -1,0 +1,300 @@
+"""Benchmark: INT8 attention + W8A8 GEMM TOPS at FLUX 1024^2 on one MI355X.
+
+A step is one pass of the hot path of one FLUX.1-schnell denoise step at
+1024 x 1024 (4096 image + 512 text tokens, 24 heads of 128): in forward order,
+19 double-stream blocks (img/txt qkv, joint INT8 attention, img/txt proj,
+img/txt MLP up and down) and 38 single-stream blocks (linear1, INT8 attention,
+linear2). Every linear is a W8A8 ``Int8Linear`` with its own random weights
+(quantize kernel + fused-epilogue GEMM); every attention is
+``attention_bhld(..., "int8_turing")``. Algorithmic work is 74.36 TOP per
+step (GEMM 2*M*N*K, attention 4*B*H*S^2*D). Inputs are resident in HBM.
+
+The same run also measures, and adds to the JSON line:
+  * per-kernel rooflines from HIP events (GEMM, attention, quantize);
+  * the full synthetic FLUX-schnell denoise step (flux_step.py) with INT8
+    attention + W8A8 linears against the same step with bf16 SDPA and bf16
+    linears, ms per step and the final-latent deviation after 4 steps;
+  * the reference's CPU path (torch CPU ops, oracle/cpu_path.py) on a bounded
+    row sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--no-full] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "INT8 attn + W8A8 GEMM TOPS (% int8 MFMA peak) at FLUX 1024²; ms/denoise step"
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- hot path
+
+class HotPath:
+    """The hot-path calls of one FLUX denoise step, in forward order."""
+
+    def __init__(self, model, shape, device):
+        from diffucore_amd import _int8
+        self.ops = []   # (kind, fn_quant, fn_gemm or fn_attn, algorithmic ops, bytes for quant)
+        dt = torch.bfloat16
+        g = torch.Generator(device=device).manual_seed(1)
+        n_img = shape.img_hw[0] * shape.img_hw[1]
+        L = n_img + shape.txt_len
+        H, D, h, m = shape.heads, shape.head_dim, shape.hidden, shape.mlp
+
+        def act(rows, cols):
+            return torch.randn(rows, cols, generator=g, device=device).to(dt)
+
+        self.acts = {
+            "img": act(n_img, h), "txt": act(shape.txt_len, h), "img_h": act(n_img, m), "txt_h": act(shape.txt_len, m),
+            "x": act(L, h), "x_h": act(L, h + m),
+        }
+        qkv = [torch.randn(1, H, L, D, generator=g, device=device).to(dt) for _ in range(3)]
+        qkv[1] += 0.5
+        self.qkv = qkv
+        attn_ops = 4 * 1 * H * L * L * D
+
+        def lin(layer, key):
+            x = self.acts[key]
+            return ("gemm", layer, x, 2 * x.shape[0] * layer.out_features * layer.in_features)
+
+        for blk in model.double_blocks:
+            for layer, key in ((blk.img_qkv, "img"), (blk.txt_qkv, "txt")):
+                self.ops.append(lin(layer, key))
+            self.ops.append(("attn", None, None, attn_ops))
+            for layer, key in ((blk.img_proj, "img"), (blk.txt_proj, "txt"), (blk.img_mlp[0], "img"),
+                               (blk.img_mlp[2], "img_h"), (blk.txt_mlp[0], "txt"), (blk.txt_mlp[2], "txt_h")):
+                self.ops.append(lin(layer, key))
+        for blk in model.single_blocks:
+            self.ops.append(lin(blk.linear1, "x"))
+            self.ops.append(("attn", None, None, attn_ops))
+            self.ops.append(lin(blk.linear2, "x_h"))
+        assert all(isinstance(op[1], _int8.Int8Linear) for op in self.ops if op[0] == "gemm")
+        self.total_ops = sum(op[3] for op in self.ops)
+        self.ws = None
+
+    def run(self):
+        from diffucore_amd import attention_bhld
+        q, k, v = self.qkv
+        for kind, layer, x, _ in self.ops:
+            if kind == "gemm":
+                layer(x)
+            else:
+                attention_bhld(q, k, v, "int8_turing")
+
+    def attribute(self):
+        """One pass with HIP events around every kernel call (torch's current
+        stream, where the kernels run): time and work per kernel kind."""
+        from diffucore_amd import _int8, attention_bhld
+        q, k, v = self.qkv
+        recs = []
+        for kind, layer, x, ops in self.ops:
+            if kind == "gemm":
+                e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+                e0.record()
+                qx, sx = _int8.quantize_activation(x, layer.group)
+                e1.record()
+                layer.matmul_quantized(qx, sx, x.dtype)
+                e2.record()
+                qbytes = x.numel() * x.element_size() + x.numel() + 4 * x.shape[0]
+                recs.append(("quant", e0, e1, 0, qbytes))
+                recs.append(("gemm", e1, e2, ops, 0))
+            else:
+                e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+                e0.record()
+                attention_bhld(q, k, v, "int8_turing")
+                e1.record()
+                recs.append(("attn", e0, e1, ops, 0))
+        torch.cuda.synchronize()
+        out = {}
+        for kind, a, b, ops, nbytes in recs:
+            d = out.setdefault(kind, {"ms": 0.0, "ops": 0, "bytes": 0, "launches": 0})
+            d["ms"] += a.elapsed_time(b)
+            d["ops"] += ops
+            d["bytes"] += nbytes
+            d["launches"] += 1
+        return out
+
+
+def time_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(shape, budget_s: float = 12.0, rows: int = 256):
+    """The reference's CPU path (oracle/cpu_path.py) on a row sample of one
+    double + one single block: W8A8 linears on ``rows`` activation rows and
+    attention for ``rows`` queries over all 4608 keys and 24 heads, repeated
+    until ``budget_s`` has elapsed."""
+    from oracle import cpu_path as C
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+    h, m, H, D = shape.hidden, shape.mlp, shape.heads, shape.head_dim
+    L = shape.img_hw[0] * shape.img_hw[1] + shape.txt_len
+    lin_shapes = [(3 * h, h)] * 2 + [(h, h)] * 2 + [(m, h), (h, m)] * 2 + [(3 * h + m, h), (h, h + m)]
+    weights = []
+    for n, k in lin_shapes:
+        w = torch.randn(n, k, generator=g) * 0.02
+        q, s = C.quantize_rows(C.rotate(w, 256))
+        x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+        weights.append((x, q, s, (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)))
+    qa = torch.randn(1, H, rows, D, generator=g)
+    ka = torch.randn(1, H, L, D, generator=g)
+    va = torch.randn(1, H, L, D, generator=g)
+    ops_per = sum(2 * rows * n * k for n, k in lin_shapes) + 2 * 4 * H * rows * L * D
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for x, q, s, b in weights:
+            C.w8a8_linear(x, q, s, b, 256)
+        for _ in range(2):
+            C.attention_bhld(qa, ka, va)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    tops = done * ops_per / el / 1e12
+    cpu = platform.processor() or "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(tops, 4), "unit": "TOPS", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"reference CPU path (torch ops: rotate+quantize_rows, torch._int_mm, rescale; fp32 SDPA) on "
+                   f"one double + one single FLUX block with {rows} activation rows per linear and {rows} "
+                   f"queries x {L} keys x {H} heads per attention, {done} repetitions in {el:.1f} s; "
+                   f"cpu '{cpu}', os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-full", action="store_true", help="skip the full FLUX step vs bf16 comparison")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
+              "run it with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import flux_step as FS
+    from diffucore_amd import _lib, quantize_linears, set_attention_backend
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _lib.require()
+    shape = FS.FluxShape()
+    log("building the synthetic FLUX.1-schnell model (bf16, random N(0,0.02))")
+    model = FS.build(shape, dev, torch.bfloat16, seed=0)
+    extra = {}
+    x0, txt, y, pe = FS.inputs(shape, dev)
+    sigmas = FS.schnell_sigmas(4, dev)
+    if not args.no_full:
+        log("full step, bf16 SDPA + bf16 linears")
+        with torch.no_grad():
+            bf16_ms = time_steps(lambda: model(x0, txt, sigmas[:1].to(x0.dtype), y, pe), 3, 1)
+            lat_bf16 = FS.denoise(model, x0, txt, y, pe, sigmas)
+    log("quantizing block linears to W8A8 (ConvRot group 256), stamping int8_turing")
+    names = FS.block_linear_names(model)
+    quantize_linears(model, names, dev, 256)
+    set_attention_backend(model, "int8_turing")
+    torch.cuda.empty_cache()
+    if not args.no_full:
+        log("full step, INT8 attention + W8A8 linears")
+        with torch.no_grad():
+            int8_ms = time_steps(lambda: model(x0, txt, sigmas[:1].to(x0.dtype), y, pe), 3, 1)
+            lat_int8 = FS.denoise(model, x0, txt, y, pe, sigmas)
+        a, b = lat_int8.float().flatten(), lat_bf16.float().flatten()
+        extra["denoise_step"] = {
+            "int8_ms": round(int8_ms, 3), "bf16_ms": round(bf16_ms, 3), "speedup": round(bf16_ms / int8_ms, 3),
+            "latent_rel_l2_vs_bf16": round(float((a - b).norm() / b.norm()), 5),
+            "latent_cos_vs_bf16": round(float(a @ b / (a.norm() * b.norm())), 6),
+            "what": "full synthetic FLUX.1-schnell forward + euler update at 1024^2 (flux_step.py), "
+                    "4-step final latent compared",
+        }
+        log(f"full step: int8 {int8_ms:.2f} ms vs bf16 {bf16_ms:.2f} ms")
+
+    hp = HotPath(model, shape, dev)
+    log(f"hot path: {len(hp.ops)} calls, {hp.total_ops / 1e12:.2f} TOP per step; timing {args.steps} steps")
+    with torch.no_grad():
+        ms = time_steps(hp.run, args.steps, args.warmup)
+        attr = hp.attribute()
+    tops = hp.total_ops / (ms * 1e-3) / 1e12
+    log(f"hot path: {ms:.3f} ms/step, {tops:.1f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% of int8 peak)")
+
+    kernels = {}
+    for kind, d in attr.items():
+        if d["ops"]:
+            kernels[kind] = {"ms": round(d["ms"], 3), "launches": d["launches"],
+                             "TOPS": round(d["ops"] / (d["ms"] * 1e-3) / 1e12, 1)}
+        else:
+            kernels[kind] = {"ms": round(d["ms"], 3), "launches": d["launches"],
+                             "GBps": round(d["bytes"] / (d["ms"] * 1e-3) / 1e9, 1)}
+    g = attr["gemm"]
+    achieved = g["ops"] / g["launches"] / (g["ms"] / g["launches"] * 1e-3) / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / "gemm_flux_step_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    roofline = {"kernel": "w8a8_gemm_kernel (all FLUX-step launches)", "bound": "mfma",
+                "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": traffic,
+                "algorithmic_ops_per_launch": g["ops"] // g["launches"],
+                "avg_launch_us": round(1e3 * g["ms"] / g["launches"], 2)}
+
+    result = {
+        "metric": METRIC, "value": round(tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "FLUX.1-schnell-shaped hot path at 1024^2: 19 double + 38 single blocks, "
+                               "4096 img + 512 txt tokens, H24 D128, W8A8 linears (ConvRot 256, bf16 out, bias) "
+                               "+ INT8 attention (bf16 in/out), one denoise step",
+                   "global_batch": 1, "seq_len": 4608, "parallelism": "none (1 GPU)",
+                   "algorithmic_TOP_per_step": round(hp.total_ops / 1e12, 3)},
+        "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
+        "kernels": kernels,
+        "roofline": roofline,
+    }
+    result.update(extra)
+    if not args.no_cpu:
+        log("CPU baseline (reference CPU path, bounded sample)")
+        result["cpu_baseline"] = cpu_baseline(shape)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
