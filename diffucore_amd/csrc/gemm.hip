@@ -10,12 +10,18 @@
 // channels n per register quad (8- or 16-byte stores in the epilogue).
 //   workgroup tile  BN x BM = (64*FN) x (64*FM), 4 waves as 2 (n) x 2 (m)
 //   wave tile       (32*FN) x (32*FM) = FN x FM MFMA blocks of 32 x 32
-//   k step          64 bytes per LDS stage, two stages, register-staged loads
-// LDS rows are 64 bytes (four 16-byte chunks); chunk c of row r sits at
-// c ^ ((r >> 1) & 3) so the 32 rows an MFMA operand read touches spread over
-// all banks. Tiles are ordered so each XCD (8 per device; the hardware deals
-// workgroups round-robin over them) works a contiguous, L2-friendly range.
+//   k depth         128 bytes per LDS stage, two stages
+// Pipeline per 128-byte k tile (4 MFMA k-steps): operand fragments for the
+// next k-step are read from LDS while the current one's MFMAs run; the next
+// tile, staged in registers, is written to the other LDS stage after the first
+// k-step; the tile after that is fetched from global memory after the second.
+// LDS rows are padded from 128 to 144 bytes so the 32 rows an operand read
+// touches spread over all banks, and every read address is a per-lane base
+// plus an immediate. Tiles are ordered so each XCD (8 per device; the hardware
+// deals workgroups round-robin over them) works a contiguous, L2-friendly range.
 #include "common.h"
+
+#include <cstdlib>
 
 namespace dc {
 
@@ -32,10 +38,9 @@ struct GemmArgs {
   int vec_out;  // 1 when 4-wide output stores are aligned
 };
 
-constexpr int BK = 64;
+constexpr int BK = 128;            // k bytes per LDS stage
+constexpr int PITCH = BK + 16;     // padded LDS row (bytes)
 constexpr int GROUP_M = 8;
-
-__device__ __forceinline__ int swz64(int c, int r) { return c ^ ((r >> 1) & 3); }
 
 template <int BIAS_DT>
 __device__ __forceinline__ float load_bias(const void* b, int n) {
@@ -51,20 +56,38 @@ __device__ __forceinline__ float epi(int acc, float sxm, float swn, const void* 
   return y;
 }
 
+// Same rounding with the bias already rounded to the output dtype (`b`).
+template <int OUT_DT, bool HAS_BIAS>
+__device__ __forceinline__ float epi_pre(int acc, float sxm, float swn, float b) {
+  float y = round_to<OUT_DT>(materialize((float)acc * (sxm * swn)));
+  if constexpr (HAS_BIAS) y = round_to<OUT_DT>(materialize(y + b));
+  return y;
+}
+
 template <int OUT_DT>
 __device__ __forceinline__ void store1(void* out, int64_t idx, float y) {
   if constexpr (OUT_DT == DC_F32) static_cast<float*>(out)[idx] = y;
   else static_cast<uint16_t*>(out)[idx] = (uint16_t)f32_to_h16<OUT_DT>(y);
 }
 
-template <int FN, int FM, int OUT_DT, int BIAS_DT>
-__global__ void __launch_bounds__(256, 1) w8a8_gemm_kernel(GemmArgs p) {
-  constexpr int BN = 64 * FN, BM = 64 * FM;
-  constexpr int WCH = BN * BK / 16, ACH = BM * BK / 16;  // 16-byte chunks per stage
-  constexpr int NWL = WCH / 256, NAL = ACH / 256;
-  static_assert(WCH % 256 == 0 && ACH % 256 == 0, "tile must split evenly over 256 threads");
-  __shared__ __attribute__((aligned(16))) int8_t sw_lds[2][BN * BK];
-  __shared__ __attribute__((aligned(16))) int8_t sa_lds[2][BM * BK];
+// Tile configuration: WN x WM waves, each owning FN x FM MFMA blocks of 32 x 32.
+template <int WN_, int WM_, int FN_, int FM_>
+struct Tile {
+  static constexpr int WN = WN_, WM = WM_, FN = FN_, FM = FM_;
+  static constexpr int NT = 64 * WN * WM;               // threads
+  static constexpr int BN = 32 * WN * FN, BM = 32 * WM * FM;
+  static constexpr int LDS = 2 * (BN + BM) * PITCH + (2 * BN + BM) * 4;
+};
+
+template <class T, int OUT_DT, int BIAS_DT>
+__global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
+  constexpr int FN = T::FN, FM = T::FM, NT = T::NT;
+  constexpr int BN = T::BN, BM = T::BM;
+  constexpr int CPR = BK / 16;                    // 16-byte chunks per row
+  constexpr int NWL = BN * CPR / NT, NAL = BM * CPR / NT;
+  static_assert(BN * CPR % NT == 0 && BM * CPR % NT == 0, "tile must split evenly over the threads");
+  constexpr int STAGE = (BN + BM) * PITCH;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int l32 = lane & 31, hf = lane >> 5;
@@ -80,8 +103,10 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_kernel(GemmArgs p) {
   const int tn = (logical % per_group) / gsize;
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const int wn = wv & 1, wm = wv >> 1;
-  const int nb = wn * 32 * FN, mb = wm * 32 * FM;
+  const int wn = wv % T::WN, wm = wv / T::WN;
+  // per-lane fragment bases: row (wave base + l32), byte 16 hf; + 32 i rows, + 32 ks bytes
+  const int wfrag = (wn * 32 * FN + l32) * PITCH + 16 * hf;
+  const int afrag = BN * PITCH + (wm * 32 * FM + l32) * PITCH + 16 * hf;
 
   v16i acc[FN][FM];
 #pragma unroll
@@ -89,98 +114,158 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = v16i{0};
 
-  uint4 wreg[NWL], areg[NAL];
+  uint4 wst[NWL], ast[NAL];
+  v4i wf[2][FN], af[2][FM];
   const int nk = (p.K + BK - 1) / BK;
 
-  auto gload = [&](int kt) {
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int u = 0; u < NWL; ++u) {
-      const int ci = t + u * 256, r = ci >> 2, c = ci & 3;
-      const int n = n0 + r, k = k0 + 16 * c;
-      wreg[u] = (n < p.N && k < p.K) ? *reinterpret_cast<const uint4*>(p.w + (int64_t)n * p.ldw + k)
-                                     : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < NAL; ++u) {
-      const int ci = t + u * 256, r = ci >> 2, c = ci & 3;
-      const int m = m0 + r, k = k0 + 16 * c;
-      areg[u] = (m < p.M && k < p.K) ? *reinterpret_cast<const uint4*>(p.a + (int64_t)m * p.lda + k)
-                                     : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto sstore = [&](int stage) {
-#pragma unroll
-    for (int u = 0; u < NWL; ++u) {
-      const int ci = t + u * 256, r = ci >> 2, c = ci & 3;
-      *reinterpret_cast<uint4*>(&sw_lds[stage][r * BK + swz64(c, r) * 16]) = wreg[u];
-    }
-#pragma unroll
-    for (int u = 0; u < NAL; ++u) {
-      const int ci = t + u * 256, r = ci >> 2, c = ci & 3;
-      *reinterpret_cast<uint4*>(&sa_lds[stage][r * BK + swz64(c, r) * 16]) = areg[u];
-    }
-  };
-
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-#pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      const int c = 2 * ks + hf;
-      v4i wf[FN], af[FM];
-#pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        const int r = nb + 32 * i + l32;
-        wf[i] = *reinterpret_cast<const v4i*>(&sw_lds[st][r * BK + swz64(c, r) * 16]);
-      }
-#pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int r = mb + 32 * j + l32;
-        af[j] = *reinterpret_cast<const v4i*>(&sa_lds[st][r * BK + swz64(c, r) * 16]);
-      }
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[i], af[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) sstore(st ^ 1);
-    __syncthreads();
+  // Row indices are clamped into range (rows past M or N only feed outputs that
+  // are never stored) and chunks past K are zeroed by a mask when they are
+  // stored to LDS, so the loads carry no branches and no waits.
+  const int64_t kmax = p.K - 16;
+#define GEMM_LOAD(kt_)                                                                                   \
+  {                                                                                                      \
+    const int k0_ = (kt_) * BK;                                                                          \
+    _Pragma("unroll") for (int u = 0; u < NWL; ++u) {                                                    \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+      const int n = min(n0 + r, p.N - 1), k = k0_ + 16 * c;                                              \
+      wst[u] = *reinterpret_cast<const uint4*>(p.w + (int64_t)n * p.ldw + min((int64_t)k, kmax));        \
+    }                                                                                                    \
+    _Pragma("unroll") for (int u = 0; u < NAL; ++u) {                                                    \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+      const int m = min(m0 + r, p.M - 1), k = k0_ + 16 * c;                                              \
+      ast[u] = *reinterpret_cast<const uint4*>(p.a + (int64_t)m * p.lda + min((int64_t)k, kmax));        \
+    }                                                                                                    \
   }
+#define GEMM_STORE(stage_, kt_)                                                                          \
+  {                                                                                                      \
+    uint8_t* base_ = smem + (stage_) * STAGE;                                                            \
+    _Pragma("unroll") for (int u = 0; u < NWL; ++u) {                                                    \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+      const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
+      const uint4 v_ = wst[u];                                                                           \
+      *reinterpret_cast<uint4*>(base_ + r * PITCH + c * 16) =                                            \
+          make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
+    }                                                                                                    \
+    _Pragma("unroll") for (int u = 0; u < NAL; ++u) {                                                    \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+      const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
+      const uint4 v_ = ast[u];                                                                           \
+      *reinterpret_cast<uint4*>(base_ + BN * PITCH + r * PITCH + c * 16) =                               \
+          make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
+    }                                                                                                    \
+  }
+#define GEMM_FRAGS(buf_, stage_, ks_)                                                                    \
+  {                                                                                                      \
+    const uint8_t* base_ = smem + (stage_) * STAGE + 32 * (ks_);                                         \
+    _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                       \
+        wf[buf_][i] = *reinterpret_cast<const v4i*>(base_ + wfrag + 32 * i * PITCH);                     \
+    _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                       \
+        af[buf_][j] = *reinterpret_cast<const v4i*>(base_ + afrag + 32 * j * PITCH);                     \
+  }
+#define GEMM_MFMAS(buf_)                                                                                 \
+  _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                         \
+  _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                         \
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[buf_][i], af[buf_][j], acc[i][j], 0, 0, 0);
+// scheduler hints: `n` MFMAs, each followed by `per` instructions of class `mask`
+#define SCHED_INTERLEAVE(n_, mask_, per_)                                                                \
+  _Pragma("unroll") for (int z = 0; z < (n_); ++z) {                                                     \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                   \
+    __builtin_amdgcn_sched_group_barrier((mask_), (per_), 0);                                            \
+  }                                                                                                      \
+  if constexpr ((n_) == 0) __builtin_amdgcn_sched_group_barrier((mask_), 64, 0);
+
+  constexpr int NF = FN + FM;                  // fragment reads per k-step
+  constexpr int NMF = FN * FM;                 // MFMAs per k-step
+  constexpr int NST = NWL + NAL;               // 16-byte stores / loads per thread per tile
+  constexpr int NSLOT = NMF > NF ? NMF - NF : 0;          // MFMAs left for stores / loads
+  constexpr int PER = NSLOT ? (NST + NSLOT - 1) / NSLOT : 1;
+  // this tile's output-channel scales, biases (rounded to the output dtype)
+  // and row scales, staged in LDS for the epilogue
+  float* sw_l = reinterpret_cast<float*>(smem + 2 * STAGE);
+  float* b_l = sw_l + BN;
+  float* sx_l = b_l + BN;
+  if constexpr (OUT_DT != DC_I32) {
+    for (int i = t; i < BN; i += NT) {
+      const int n = min(n0 + i, p.N - 1);
+      sw_l[i] = p.sw[n];
+      if constexpr (BIAS_DT != DC_NONE) b_l[i] = round_to<OUT_DT>(load_bias<BIAS_DT>(p.bias, n));
+    }
+    for (int i = t; i < BM; i += NT) sx_l[i] = p.sx[min(m0 + i, p.M - 1)];
+  }
+  GEMM_LOAD(0);
+  GEMM_STORE(0, 0);
+  GEMM_LOAD(1);
+  __syncthreads();
+  GEMM_FRAGS(0, 0, 0);
+  // Each k-step is its own scheduling region: its MFMAs consume fragments read
+  // one k-step earlier while it issues the reads for the next one. Barrier A
+  // (all waves stored tile kt + 1) lets k-step 3 prefetch tile kt + 1's first
+  // fragments; barrier B (all waves done reading stage cur) guards the next
+  // iteration's store into it.
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    GEMM_FRAGS(1, cur, 1);
+    GEMM_MFMAS(0);
+    GEMM_STORE(cur ^ 1, kt + 1);
+    SCHED_INTERLEAVE(NF, 0x100, 1);
+    SCHED_INTERLEAVE(NSLOT, 0x200, PER);
+    __builtin_amdgcn_sched_barrier(0);
+    GEMM_FRAGS(0, cur, 2);
+    GEMM_MFMAS(1);
+    GEMM_LOAD(kt + 2);
+    SCHED_INTERLEAVE(NF, 0x100, 1);
+    SCHED_INTERLEAVE(NSLOT, 0x020, PER);
+    __builtin_amdgcn_sched_barrier(0);
+    GEMM_FRAGS(1, cur, 3);
+    GEMM_MFMAS(0);
+    SCHED_INTERLEAVE(NF, 0x100, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();   // A
+    GEMM_FRAGS(0, cur ^ 1, 0);
+    GEMM_MFMAS(1);
+    SCHED_INTERLEAVE(NF, 0x100, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();   // B
+  }
+#undef SCHED_INTERLEAVE
+#undef GEMM_MFMAS
+#undef GEMM_LOAD
+#undef GEMM_STORE
+#undef GEMM_FRAGS
 
   // epilogue: acc[i][j] register r -> n = n0 + nb + 32 i + 8 (r / 4) + 4 hf + r % 4, m = m0 + mb + 32 j + l32
+  const int nb = wn * 32 * FN, mb = wm * 32 * FM;
+  const bool full = p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
-    const int m = m0 + mb + 32 * j + l32;
-    if (m >= p.M) continue;
+    const int ml = mb + 32 * j + l32, m = m0 + ml;
+    if (!full && m >= p.M) continue;
     float sxm = 0.0f;
-    if constexpr (OUT_DT != DC_I32) sxm = p.sx[m];
+    if constexpr (OUT_DT != DC_I32) sxm = sx_l[ml];
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = n0 + nb + 32 * i + 8 * g + 4 * hf;
-        if (n >= p.N) continue;
+        const int nl = nb + 32 * i + 8 * g + 4 * hf, n = n0 + nl;
         const int64_t base = (int64_t)m * p.ldo + n;
-        const int a0 = acc[i][j][4 * g], a1 = acc[i][j][4 * g + 1], a2 = acc[i][j][4 * g + 2], a3 = acc[i][j][4 * g + 3];
+        const int av[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
         if constexpr (OUT_DT == DC_I32) {
           int* o = static_cast<int*>(p.out);
-          if (p.vec_out && n + 3 < p.N) {
-            *reinterpret_cast<int4*>(o + base) = make_int4(a0, a1, a2, a3);
+          if (full || (p.vec_out && n + 3 < p.N)) {
+            *reinterpret_cast<int4*>(o + base) = make_int4(av[0], av[1], av[2], av[3]);
           } else {
-            const int av[4] = {a0, a1, a2, a3};
             for (int e = 0; e < 4 && n + e < p.N; ++e) o[base + e] = av[e];
           }
         } else {
-          if (p.vec_out && n + 3 < p.N) {
-            const float4 s4 = *reinterpret_cast<const float4*>(p.sw + n);
-            const float y0 = epi<OUT_DT, BIAS_DT>(a0, sxm, s4.x, p.bias, n);
-            const float y1 = epi<OUT_DT, BIAS_DT>(a1, sxm, s4.y, p.bias, n + 1);
-            const float y2 = epi<OUT_DT, BIAS_DT>(a2, sxm, s4.z, p.bias, n + 2);
-            const float y3 = epi<OUT_DT, BIAS_DT>(a3, sxm, s4.w, p.bias, n + 3);
+          const float4 s4 = *reinterpret_cast<const float4*>(sw_l + nl);
+          float4 b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+          if constexpr (BIAS_DT != DC_NONE) b4 = *reinterpret_cast<const float4*>(b_l + nl);
+          constexpr bool HB = BIAS_DT != DC_NONE;
+          const float y0 = epi_pre<OUT_DT, HB>(av[0], sxm, s4.x, b4.x);
+          const float y1 = epi_pre<OUT_DT, HB>(av[1], sxm, s4.y, b4.y);
+          const float y2 = epi_pre<OUT_DT, HB>(av[2], sxm, s4.z, b4.z);
+          const float y3 = epi_pre<OUT_DT, HB>(av[3], sxm, s4.w, b4.w);
+          if (full || (p.vec_out && n + 3 < p.N)) {
             if constexpr (OUT_DT == DC_F32) {
               *reinterpret_cast<float4*>(static_cast<float*>(p.out) + base) = make_float4(y0, y1, y2, y3);
             } else {
@@ -189,9 +274,8 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_kernel(GemmArgs p) {
               *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + base) = make_uint2(lo, hi);
             }
           } else {
-            const int av[4] = {a0, a1, a2, a3};
-            for (int e = 0; e < 4 && n + e < p.N; ++e)
-              store1<OUT_DT>(p.out, base + e, epi<OUT_DT, BIAS_DT>(av[e], sxm, p.sw[n + e], p.bias, n + e));
+            const float yv[4] = {y0, y1, y2, y3};
+            for (int e = 0; e < 4 && n + e < p.N; ++e) store1<OUT_DT>(p.out, base + e, yv[e]);
           }
         }
       }
@@ -214,13 +298,23 @@ __global__ void __launch_bounds__(256) rescale_kernel(const int32_t* __restrict_
     store1<OUT_DT>(out, m * ldo + n + e, epi<OUT_DT, BIAS_DT>(acc[m * lda + n + e], sxm, sw[n + e], bias, n + e));
 }
 
-template <int FN, int FM, int OUT_DT, int BIAS_DT>
+template <class T, int OUT_DT, int BIAS_DT>
 static int launch_gemm(GemmArgs p, hipStream_t st) {
-  p.tiles_n = (p.N + 64 * FN - 1) / (64 * FN);
-  p.tiles_m = (p.M + 64 * FM - 1) / (64 * FM);
+  p.tiles_n = (p.N + T::BN - 1) / T::BN;
+  p.tiles_m = (p.M + T::BM - 1) / T::BM;
   const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
   if (tiles > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm: problem too large");
-  hipLaunchKernelGGL((w8a8_gemm_kernel<FN, FM, OUT_DT, BIAS_DT>), dim3((unsigned)tiles), dim3(256), 0, st, p);
+  static bool attr_set = false;   // per instantiation; the attribute is process-wide
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w8a8_gemm_kernel<T, OUT_DT, BIAS_DT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS);
+    if (e != hipSuccess) {
+      set_error("w8a8_gemm_kernel: cannot reserve %d bytes of LDS: %s", T::LDS, hipGetErrorString(e));
+      return DC_EHIP;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((w8a8_gemm_kernel<T, OUT_DT, BIAS_DT>), dim3((unsigned)tiles), dim3(T::NT), T::LDS, st, p);
   return launch_status("w8a8_gemm_kernel");
 }
 
@@ -228,8 +322,10 @@ template <int OUT_DT, int BIAS_DT>
 static int pick_tile(GemmArgs p, hipStream_t st) {
   // 256 x 256 tiles while they fill the device; smaller tiles for small problems
   const int64_t big = (int64_t)((p.N + 255) / 256) * ((p.M + 255) / 256);
-  if (big >= 192) return launch_gemm<4, 4, OUT_DT, BIAS_DT>(p, st);
-  return launch_gemm<2, 2, OUT_DT, BIAS_DT>(p, st);
+  static const int cfg = getenv("DC_GEMM_CFG") ? atoi(getenv("DC_GEMM_CFG")) : 0;
+  if (cfg == 1) return launch_gemm<Tile<2, 2, 4, 4>, OUT_DT, BIAS_DT>(p, st);
+  if (big >= 192) return launch_gemm<Tile<2, 4, 4, 2>, OUT_DT, BIAS_DT>(p, st);
+  return launch_gemm<Tile<2, 2, 2, 2>, OUT_DT, BIAS_DT>(p, st);
 }
 
 template <int OUT_DT>

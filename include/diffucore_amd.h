@@ -78,7 +78,7 @@ int dc_rescale(const int32_t* acc, int64_t lda, const float* sx, const float* sw
                int64_t M, int64_t N, void* stream);
 
 /*
- * Workspace size in bytes for dc_int8_attn_fwd at this shape.
+ * Workspace size in bytes for dc_int8_attn_fwd at this shape (Lq is unused).
  * Replaces the scratch tensors fwd allocates itself
  * (src/diffucore/kernels/int8_attn_sm80.cu:469-476).
  */
@@ -93,23 +93,31 @@ size_t dc_int8_attn_workspace_bytes(int B, int H, int Lq, int Lk, int D);
  *   D is contiguous. D % 8 == 0, D <= 128, strides % 8 == 0, 16-byte aligned.
  *   sm_scale: softmax scale (the reference passes D ** -0.5).
  * K is smoothed by its per-channel mean and quantized per 64-key block; Q is
- * quantized per token; S = Q K^T runs on int8 MFMA into int32; the online
- * softmax is float32 in base 2; P V runs on 16-bit MFMA with float32
- * accumulation. The workspace (dc_int8_attn_workspace_bytes) holds, at
- * 256-byte aligned offsets in this order:
- *   q8  int8 [B, H, Lq128, Dp]   Lq128 = Lq rounded up to 128, Dp = 64 or 128
- *   qs  f32  [B, H, Lq128]       per-token scale amax / 127
- *   k8  int8 [B, H, Lk64, Dp]    Lk64 = Lk rounded up to 64
- *   ks  f32  [B, H, Lk64 / 64]   per-block scale amax / 127
- *   vt  16-bit [B, H, Dp, Lk64]  V transposed (MFMA operand order)
- *   kpart f32 [B, H, ceil(Lk / 128), D]   per-window key sums
- *   ksum  f32 [B, H, D]                    per-channel key sums
+ * quantized per token inside the attention kernel; S = Q K^T runs on int8
+ * MFMA into int32; the online softmax is float32 in base 2; P V runs on
+ * 16-bit MFMA with float32 accumulation. The workspace
+ * (dc_int8_attn_workspace_bytes) holds, at 256-byte aligned offsets in order:
+ *   k8    int8 [B, H, Lk64, Dp]   Lk64 = Lk rounded up to 64, Dp = 64 or 128
+ *   ks    f32  [B, H, Lk64 / 64]  per-block scale amax / 127
+ *   kpart f32  [B, H, ceil(Lk / 128), D]   per-window key sums
+ *   ksum  f32  [B, H, D]                    per-channel key sums
  */
 int dc_int8_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B,
                      int H, int Lq, int Lk, int D, const int64_t q_strides[3],
                      const int64_t k_strides[3], const int64_t v_strides[3],
                      const int64_t o_strides[3], float sm_scale, void* workspace,
                      size_t ws_bytes, void* stream);
+
+/*
+ * The per-token Q quantizer of dc_int8_attn_fwd (the same device code), with
+ * its codes written out for verification: q8 int8 [B, H, Lq32, Dp] and
+ * qs f32 [B, H, Lq32] = amax / 127, Lq32 = Lq rounded up to 32; rows past Lq
+ * and channels past D are 0. Replaces the Q prologue of the reference's
+ * attn_kernel (src/diffucore/kernels/int8_attn_sm80.cu:341-388), which keeps
+ * its codes in registers.
+ */
+int dc_int8_attn_quantize_q(const void* q, int dtype, int B, int H, int Lq, int D,
+                            const int64_t q_strides[3], int8_t* q8, float* qs, void* stream);
 
 #ifdef __cplusplus
 }
