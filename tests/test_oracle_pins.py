@@ -1,0 +1,300 @@
+"""Pins of the CPU oracle (no GPU): each oracle function is checked against an
+independent computation - exact rational arithmetic, float64 with a single
+final rounding, explicit matrices, brute-force loops over the reference's
+literal loop structure, textbook special cases - and a planted mistake shows
+the check would catch the plausible bug. The reference ships no numeric golden
+vectors for this path (its only bit-exact contract is
+``tests/test_int8.py:174-183``), so these pins are the oracle's anchor.
+"""
+
+from __future__ import annotations
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attn as OA
+from oracle import cpu_path as OC
+from oracle import fp as OF
+from oracle import gemm as OG
+from oracle import quant as OQ
+
+RNG = np.random.default_rng(1234)
+
+
+def _f32(x):
+    return np.asarray(x, np.float32)
+
+
+def _round_exact_to_f32(q: Fraction) -> np.float32:
+    """Nearest float32 to an exact rational (ties to even), by comparing the
+    two float32 neighbours exactly."""
+    f = np.float32(float(q))           # within one ulp of the answer
+    cands = {f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))}
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - q), int(np.array(c).view(np.int32)) & 1))
+    return np.float32(best)
+
+
+# ---------------------------------------------------------------- float helpers
+
+def test_fma_f32_matches_exact_rational_rounding():
+    a = _f32(RNG.standard_normal(400) * 3)
+    b = _f32(RNG.standard_normal(400) / 7)
+    c = _f32(RNG.standard_normal(400))
+    # hard cases: c ~= -a*b so the result is dominated by the product's low bits
+    c[:100] = -(a[:100].astype(np.float64) * b[:100]).astype(np.float32)
+    got = OF.fma_f32(a, b, c)
+    for i in range(400):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        assert got[i] == _round_exact_to_f32(exact), i
+    # a separate multiply and add (two roundings) differs somewhere on these inputs
+    two = (a * b).astype(np.float32) + c
+    assert (two != got).any()
+
+
+def test_bf16_rounding_ties_to_even_and_specials():
+    x = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 1.0 + 2 ** -8 + 2 ** -20, -2.5, 0.0, -0.0, np.inf, 3e38],
+                 np.float32)
+    got = OF.round_bf16(x)
+    assert got[0] == 1.0                       # tie -> even mantissa
+    assert got[1] == 1.0 + 4 * 2 ** -8         # tie -> even (up)
+    assert got[2] == 1.0 + 2 * 2 ** -8         # above the tie -> up
+    assert got[3] == -2.5 and got[4] == 0 and np.isinf(got[6])
+    assert np.isnan(OF.round_bf16(np.array([np.nan], np.float32)))[0]
+    # agrees with torch's bfloat16 conversion on random values
+    r = _f32(RNG.standard_normal(10000) * 100)
+    assert np.array_equal(OF.round_bf16(r), torch.tensor(r).bfloat16().float().numpy())
+
+
+# ---------------------------------------------------------------- quantizer
+
+def test_quantize_rows_against_float64_and_properties():
+    x = _f32(RNG.standard_normal((64, 320)))
+    x[:, RNG.permutation(320)[:2]] *= 20        # outlier channels
+    x[5] = 0
+    q, s = OQ.quantize_rows(x)
+    amax = np.abs(x.astype(np.float64)).max(1)
+    s_ref = np.maximum((amax / 127.0).astype(np.float32), np.float32(1e-30))   # one rounding of the exact quotient
+    assert np.array_equal(s, s_ref)
+    quot = (x.astype(np.float64) / s_ref.astype(np.float64)[:, None]).astype(np.float32)   # correctly rounded x/s
+    assert np.array_equal(q, np.clip(np.rint(quot), -128, 127).astype(np.int8))
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    nz = amax > 0
+    assert (np.abs(q[nz].astype(np.int32)).max(1) == 127).all()
+    assert s[5] == np.float32(1e-30) and not q[5].any()
+
+
+def test_quantize_rows_ties_round_to_even():
+    # x / scale lands exactly on k + 0.5 for these values: scale = 1 (amax 127)
+    x = _f32([[127.0, 2.5, 3.5, -2.5, -0.5, 0.5, 1.5, 0.0]])
+    q, s = OQ.quantize_rows(x)
+    assert s[0] == 1.0
+    assert q.tolist() == [[127, 2, 4, -2, 0, 0, 2, 0]]
+    # planted mistake: round-half-away-from-zero would give 3, 4, -3, -1, 1, 2
+    away = np.sign(x) * np.floor(np.abs(x) + 0.5)
+    assert not np.array_equal(away.astype(np.int8), q)
+
+
+def test_torch_cpu_path_and_numpy_oracle_agree():
+    """Two independent statements of ``_quantize_rows`` (torch ops as the
+    reference writes them, numpy ops in the oracle) are bit-identical."""
+    x = torch.randn(200, 768) * 3
+    q_t, s_t = OC.quantize_rows(x)
+    q_n, s_n = OQ.quantize_rows(x.numpy())
+    assert np.array_equal(q_t.numpy(), q_n) and np.array_equal(s_t.numpy(), s_n)
+
+
+def test_hadamard_symmetric_self_inverse():
+    h = OQ.hadamard(256)
+    assert np.array_equal(h, h.T)
+    np.testing.assert_allclose(h.astype(np.float64) @ h, np.eye(256), atol=1e-6)
+    assert np.array_equal(OQ.hadamard(256), OC.hadamard(256).numpy())
+
+
+def test_butterfly_equals_explicit_hadamard():
+    # exact on basis vectors: e_i @ H is row i of H (every entry +-1/16)
+    e = np.eye(256, dtype=np.float32)
+    assert np.array_equal(OQ.rotate_butterfly(e, 256), OQ.hadamard(256))
+    # close to the float64 product on random rows, and linear
+    x = _f32(RNG.standard_normal((16, 512)))
+    ref = (x.astype(np.float64).reshape(16, 2, 256) @ OQ.hadamard(256).astype(np.float64)).reshape(16, 512)
+    np.testing.assert_allclose(OQ.rotate_butterfly(x, 256), ref, rtol=0, atol=2e-6)
+    # planted mistake: H4 applied with the wrong sign pattern (S - 2 x[j] instead of S - 2 x[3-j])
+    y = x.reshape(16, 2, 4, 64)
+    s = (y[:, :, 0] + y[:, :, 1]) + (y[:, :, 2] + y[:, :, 3])
+    wrong = np.stack([s - 2 * y[:, :, j] for j in range(4)], 2).reshape(16, 512)
+    right_first_axis = np.stack([s - 2 * y[:, :, 3 - j] for j in range(4)], 2).reshape(16, 512)
+    assert not np.allclose(wrong, right_first_axis)
+
+
+def test_convrot_codes_match_matmul_form_closely():
+    x = _f32(RNG.standard_normal((256, 3072)))
+    q_b, s_b = OQ.quantize_activation(x, 256)
+    q_m, s_m = OQ.quantize_rows(OQ.rotate_matmul(x, 256))
+    d = np.abs(q_b.astype(np.int32) - q_m.astype(np.int32))
+    assert d.max() <= 1 and (d != 0).mean() < 1e-2
+    np.testing.assert_allclose(s_b, s_m, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- GEMM epilogue
+
+def test_int_mm_exact_against_python_ints():
+    q = RNG.integers(-127, 128, (7, 48), dtype=np.int8)
+    w = RNG.integers(-127, 128, (5, 48), dtype=np.int8)
+    ref = [[sum(int(a) * int(b) for a, b in zip(q[i], w[j])) for j in range(5)] for i in range(7)]
+    assert OG.int_mm(q, w).tolist() == ref
+    big = np.full((1, 4096), 127, np.int8)
+    assert OG.int_mm(big, big)[0, 0] == 4096 * 127 * 127
+
+
+def test_rescale_closed_forms():
+    # int32 -> float32 is round-to-nearest-even above 2^24
+    acc = np.array([[2 ** 24 + 1, 2 ** 24 + 3, -(2 ** 24 + 1), 7]], np.int32)
+    y = OG.rescale(acc, _f32([1.0]), _f32([1.0, 1.0, 1.0, 0.25]), None, "f32")
+    assert y.tolist() == [[2 ** 24, 2 ** 24 + 4, -(2 ** 24), 1.75]]
+    # the fp16 tie the GPU epilogue once got wrong: float32 -0.2623291 is the
+    # midpoint of two fp16 values and rounds to the even one
+    acc = np.array([[1]], np.int32)
+    yy = OG.rescale(acc, _f32([-0.2623291015625]), _f32([1.0]), None, "f16")
+    assert np.float16(yy[0, 0]).view(np.uint16) == 0xB432
+    # bias double rounding: round(round(y) + round(b)) differs from round(y + b)
+    acc = np.array([[1]], np.int32)
+    sx, sw = _f32([1.0 + 3 * 2 ** -10]), _f32([1.0])
+    b = _f32([3 * 2 ** -10])
+    two = OG.rescale(acc, sx, sw, b, "bf16")[0, 0]
+    single = OF.round_bf16(np.float32(1.0 + 6 * 2 ** -10))
+    assert two == 1.0 and single == np.float32(1.0 + 2 ** -7)
+
+
+def test_rescale_matches_torch_reference_statement():
+    acc = torch.randint(-2 ** 28, 2 ** 28, (33, 40), dtype=torch.int32)
+    sx, sw = torch.rand(33) * 1e-3, torch.rand(40) * 1e-3
+    bias = torch.randn(40).bfloat16()
+    for dt, name in ((torch.float16, "f16"), (torch.bfloat16, "bf16"), (torch.float32, "f32")):
+        ref = OC.rescale(acc, sx, sw, bias, dt).float().numpy()
+        got = OG.rescale(acc.numpy(), sx.numpy(), sw.numpy(), bias.float().numpy(), name)
+        assert np.array_equal(got, ref), name
+
+
+# ---------------------------------------------------------------- attention prep
+
+def _colsum_literal(k):
+    """The reference's loops (int8_attn_sm80.cu:100-142), one float32 add at a time."""
+    k = _f32(k)
+    B, L, H, D = k.shape
+    nwin = -(-L // 128)
+    out = np.zeros((B, H, D), np.float32)
+    for b in range(B):
+        for h in range(H):
+            for d in range(D):
+                total = np.float32(0)
+                for w in range(nwin):
+                    parts = []
+                    for rg in range(16):
+                        a = np.float32(0)
+                        for r in range(w * 128 + rg, min(L, w * 128 + 128), 16):
+                            a = np.float32(a + k[b, r, h, d])
+                        parts.append(a)
+                    sk = np.float32(0)
+                    for a in parts:
+                        sk = np.float32(sk + a)
+                    total = np.float32(total + sk)
+                out[b, h, d] = total
+    return out
+
+
+def test_k_colsum_matches_literal_loop_order():
+    k = _f32(torch.randn(1, 300, 2, 8).half().float().numpy() + 0.5)
+    assert np.array_equal(OA.k_colsum(k), _colsum_literal(k))
+    np.testing.assert_allclose(OA.k_colsum(k), k.astype(np.float64).sum(1), rtol=1e-5)
+
+
+def test_k_quantize_properties_and_fma_choice():
+    k = torch.randn(2, 150, 3, 40).bfloat16().float().numpy() + 0.7
+    ksum = OA.k_colsum(k)
+    ki, ks = OA.k_quantize(k, ksum)
+    assert ki.shape == (2, 3, 192, 40) and ks.shape == (2, 3, 3)
+    assert not ki[:, :, 150:].any()
+    blocks = np.abs(ki.astype(np.int32)).reshape(2, 3, 3, -1).max(-1)
+    assert (blocks == 127).all() and np.abs(ki.astype(np.int32)).max() <= 127
+    val = OA.k_smooth(k, ksum)
+    amax = np.abs(np.concatenate([val, np.zeros((2, 3, 42, 40), np.float32)], 2).reshape(2, 3, 3, -1)).max(-1)
+    assert np.array_equal(ks, (amax / np.float32(127)).astype(np.float32))
+    # the smoothing is one rounding of k - ksum/L's exact product form
+    inv_l = np.float32(1) / np.float32(150)
+    exact = np.array([[_round_exact_to_f32(Fraction(float(k[0, r, 0, d])) - Fraction(float(ksum[0, 0, d])) *
+                                           Fraction(float(inv_l))) for d in range(40)] for r in range(4)])
+    assert np.array_equal(val[0, 0, :4], exact)
+    # against the unfused form the codes differ in at most a few places, by one
+    unfused = (k.transpose(0, 2, 1, 3) - (ksum[:, :, None, :] * inv_l).astype(np.float32)).astype(np.float32)
+    assert np.abs(unfused - val).max() <= 2 * np.spacing(np.abs(val).max())
+
+
+def test_q_quantize_properties():
+    q = torch.randn(1, 100, 2, 64).bfloat16().float().numpy()
+    q[0, 7, 1] = 0
+    q8, qs = OA.q_quantize(q)
+    assert (np.abs(q8.astype(np.int32)).max(-1)[qs > 0] == 127).all()
+    assert qs[0, 1, 7] == 0 and not q8[0, 1, 7].any()
+
+
+# ---------------------------------------------------------------- attention output
+
+def _sdpa(q, k, v):
+    t = [torch.tensor(x).transpose(1, 2) for x in (q, k, v)]
+    return F.scaled_dot_product_attention(*t).transpose(1, 2).numpy()
+
+
+def test_int8_attention_special_cases():
+    k = _f32(RNG.standard_normal((1, 50, 1, 64)))
+    v = _f32(RNG.standard_normal((1, 50, 1, 64)))
+    # zero queries: uniform weights, output is the mean of V
+    out = OA.int8_attention(np.zeros((1, 3, 1, 64), np.float32), k, v, None, "f16", "f32")
+    np.testing.assert_allclose(out[0, :, 0], np.broadcast_to(v[0, :, 0].mean(0), (3, 64)), atol=1e-6)
+    # a single key: output is that key's value row (rounded to the output type)
+    out1 = OA.int8_attention(_f32(RNG.standard_normal((1, 4, 1, 64))), k[:, :1], v[:, :1], None, "bf16", "bf16")
+    assert np.array_equal(out1[0, :, 0], np.broadcast_to(OF.round_bf16(v[0, 0, 0]), (4, 64)))
+
+
+def test_int8_attention_close_to_sdpa_reference_bar():
+    q = _f32(RNG.standard_normal((1, 200, 2, 128)))
+    k = _f32(RNG.standard_normal((1, 300, 2, 128)) + 0.5)
+    v = _f32(RNG.standard_normal((1, 300, 2, 128)))
+    o = OA.int8_attention(q, k, v, None, "f16", "f32").astype(np.float64)
+    ref = _sdpa(q, k, v).astype(np.float64)
+    rel = np.linalg.norm(o - ref) / np.linalg.norm(ref)
+    cos = (o.ravel() @ ref.ravel()) / (np.linalg.norm(o) * np.linalg.norm(ref))
+    assert rel < 3e-2 and cos > 0.9995
+
+
+def test_dropping_k_smoothing_fails_the_bar(monkeypatch):
+    """Planted mistake: without the K mean subtraction a large key offset eats
+    the int8 range and the result misses the reference's bar; with it, the
+    same inputs pass."""
+    q = _f32(RNG.standard_normal((1, 64, 1, 128)))
+    k = _f32(RNG.standard_normal((1, 256, 1, 128)) + 20.0)
+    v = _f32(RNG.standard_normal((1, 256, 1, 128)))
+    ref = _sdpa(q, k, v).astype(np.float64)
+
+    def rel(o):
+        o = o.astype(np.float64)
+        return np.linalg.norm(o - ref) / np.linalg.norm(ref)
+
+    assert rel(OA.int8_attention(q, k, v, None, "bf16", "f32")) < 3e-2
+    monkeypatch.setattr(OA, "k_colsum", lambda kk: np.zeros((1, 1, 128), np.float32))
+    assert rel(OA.int8_attention(q, k, v, None, "bf16", "f32")) > 3e-2
+
+
+@pytest.mark.parametrize("shift", [0.0, 40.0])
+def test_int8_attention_is_shift_invariant_in_keys(shift):
+    """Adding a constant vector to every key leaves softmax(q.k) unchanged; the
+    mean smoothing removes it before quantization, so the codes are the same."""
+    q = _f32(RNG.standard_normal((1, 20, 1, 64)))
+    k = _f32(RNG.standard_normal((1, 64, 1, 64)))
+    v = _f32(RNG.standard_normal((1, 64, 1, 64)))
+    base = OA.int8_attention(q, k, v, None, "bf16", "f32")
+    shifted = OA.int8_attention(q, (k + np.float32(shift)).astype(np.float32), v, None, "bf16", "f32")
+    np.testing.assert_allclose(shifted, base, atol=3e-2)

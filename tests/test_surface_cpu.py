@@ -1,0 +1,218 @@
+"""The operator surface on the CPU (no GPU): dispatch semantics of the
+reference's attention module (``tests/test_attention_dispatch.py``), the
+load-time parts of ``Int8Linear`` (``tests/test_int8.py:40-71``), the C ABI's
+exported symbols and argument checks, and the absence of any CPU fallback
+on the W8A8 hot path."""
+
+from __future__ import annotations
+
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+import diffucore_amd as D
+from diffucore_amd import _attention, _int8, _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+_CPU = D.DevicePolicy(device=torch.device("cpu"), compute_dtype=torch.float32)
+
+
+def _rel(a, b):
+    return ((a.float() - b.float()).norm() / b.float().norm()).item()
+
+
+# ---------------------------------------------------------------- attention dispatch
+
+def _ref_blhd(q, k, v):
+    out = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    return out.transpose(1, 2).reshape(q.shape[0], q.shape[1], -1)
+
+
+def test_sdpa_branches_are_exact():
+    torch.manual_seed(0)
+    q, k, v = torch.randn(2, 64, 4, 32), torch.randn(2, 48, 4, 32), torch.randn(2, 48, 4, 32)
+    assert torch.equal(D.attention_blhd(q, k, v, "sdpa"), _ref_blhd(q, k, v))
+    qh, kh, vh = (torch.randn(2, 4, 64, 32) for _ in range(3))
+    ref = F.scaled_dot_product_attention(qh, kh, vh).transpose(1, 2).reshape(2, 64, -1)
+    assert torch.equal(D.attention_bhld(qh, kh, vh, "sdpa"), ref)
+
+
+def test_int8_backend_falls_back_off_gpu():
+    q = torch.randn(1, 16, 2, 128)
+    assert torch.equal(D.attention_blhd(q, q, q, "int8_turing"), D.attention_blhd(q, q, q, "sdpa"))
+    qh = torch.randn(1, 2, 16, 64)
+    assert torch.equal(D.attention_bhld(qh, qh, qh, "int8_turing"), D.attention_bhld(qh, qh, qh, "sdpa"))
+
+
+def test_null_keys_equal_padded():
+    torch.manual_seed(0)
+    q, k, v = torch.randn(1, 30, 4, 64), torch.randn(1, 7, 4, 64), torch.randn(1, 7, 4, 64)
+    pad = (0, 0, 0, 0, 0, 5)
+    assert torch.equal(D.attention_blhd(q, k, v, null_keys=5), D.attention_blhd(q, F.pad(k, pad), F.pad(v, pad)))
+
+
+def test_policy_resolution():
+    assert D.resolve_attention_backend(_CPU) == "sdpa"
+    auto = D.DevicePolicy(device=torch.device("cpu"), compute_dtype=torch.float32, attention="auto")
+    assert D.resolve_attention_backend(auto) == "sdpa"
+    for attn in ("int8_turing", "fa2_turing"):
+        pol = D.DevicePolicy(device=torch.device("cpu"), compute_dtype=torch.float32, attention=attn)
+        with pytest.raises(ValueError, match=attn):
+            D.resolve_attention_backend(pol)
+    pol = D.DevicePolicy(device=torch.device("cpu"), compute_dtype=torch.float16, attention="int8_turing",
+                         compile=True)
+    with pytest.raises(ValueError, match="compile"):
+        D.resolve_attention_backend(pol)
+    with pytest.raises(ValueError, match="attention"):
+        D.DevicePolicy(device=torch.device("cpu"), attention="flash3")
+
+
+def test_int8_requirements_on_a_gfx950_policy(monkeypatch):
+    """With the device checks satisfied, the remaining requirement messages are
+    the dtype and compile ones (and a missing library would be named)."""
+    monkeypatch.setattr(_attention, "_is_gfx950", lambda d=None: True)
+    pol = D.DevicePolicy(device=torch.device("cuda"), compute_dtype=torch.float32, attention="int8_turing")
+    with pytest.raises(ValueError, match="fp16 or bf16"):
+        D.resolve_attention_backend(pol)
+    pol = D.DevicePolicy(device=torch.device("cuda"), compute_dtype=torch.bfloat16, attention="int8_turing")
+    if _lib.lib() is not None:
+        assert D.resolve_attention_backend(pol) == "int8_turing"
+    monkeypatch.setattr(_lib, "lib", lambda: None)
+    monkeypatch.setattr(_lib, "load_error", lambda: "libdiffucore_amd.so is not built")
+    with pytest.raises(ValueError, match="not built"):
+        D.resolve_attention_backend(pol)
+
+
+class _SelfAttn(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.attn_backend = "sdpa"
+
+
+class _CrossAttn(_SelfAttn):
+    is_selfattn = False
+
+
+def test_stamping_self_and_cross_attention():
+    holder = nn.ModuleList([_SelfAttn(), _CrossAttn(), nn.Linear(2, 2), _SelfAttn()])
+    assert D.set_attention_backend(holder, "int8_turing") == 3
+    assert [getattr(m, "attn_backend", None) for m in holder] == ["int8_turing", "sdpa", None, "int8_turing"]
+    assert D.set_attention_backend(holder, "sdpa") == 3
+
+
+def test_flux_harness_stamps_and_swaps():
+    import flux_step as FS
+    shape = FS.FluxShape(hidden=256, heads=2, depth=2, depth_single=3, context_dim=64, vec_dim=32,
+                         axes=(16, 56, 56), img_hw=(4, 4), txt_len=8)
+    with torch.device("meta"):
+        model = FS.FluxDiT(shape)
+    assert D.set_attention_backend(model, "int8_turing") == 5
+    names = FS.block_linear_names(model)
+    assert len(names) == 2 * 8 + 3 * 2
+    assert all(isinstance(model.get_submodule(n), nn.Linear) for n in names)
+
+
+# ---------------------------------------------------------------- Int8Linear (load time)
+
+def test_hadamard_is_symmetric_and_self_inverse():
+    h = _int8._hadamard(256, "cpu")
+    torch.testing.assert_close(h, h.T)
+    torch.testing.assert_close(h @ h, torch.eye(256), atol=1e-6, rtol=0)
+
+
+def test_weight_round_trip_and_to_linear():
+    torch.manual_seed(0)
+    w = torch.randn(64, 512) * 0.02
+    for group in (0, 256):
+        q, s = D.quantize_weight(w, group)
+        assert _rel(D.dequantize_weight(q, s, group), w) < 0.01
+    lin = nn.Linear(512, 64)
+    m = D.Int8Linear.from_linear(lin)
+    back = m.to_linear(torch.float32)
+    assert _rel(back.weight, lin.weight) < 0.01 and torch.equal(back.bias, lin.bias)
+
+
+def test_scale_survives_dtype_cast():
+    m = D.Int8Linear.from_linear(nn.Linear(256, 32))
+    s = m.scale.clone()
+    m.to(torch.float16)
+    assert m.weight.dtype == torch.int8 and torch.equal(m.scale, s)
+
+
+def test_group_must_divide_in_features():
+    with pytest.raises(ValueError, match="multiple"):
+        D.Int8Linear(320, 64, group=256)
+
+
+def test_hot_path_has_no_cpu_fallback():
+    m = D.Int8Linear.from_linear(nn.Linear(256, 32))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        m(torch.randn(3, 256))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        D.quantize_activation(torch.randn(3, 256), 256)
+    assert D.scaled_mm(torch.zeros(3, 16, dtype=torch.int8), torch.zeros(8, 16, dtype=torch.int8),
+                       torch.ones(3), torch.ones(8), torch.float16) is None
+
+
+def test_quantize_and_dequantize_linears():
+    model = nn.Sequential(nn.Linear(512, 256), nn.GELU(), nn.Linear(256, 64))
+    assert D.quantize_linears(model, ["0", "2"], "cpu", group=0) == 2
+    assert isinstance(model[0], D.Int8Linear) and model[0].group == 0
+    assert _int8.dequantize_linears(model, torch.float32) == 2
+    assert type(model[0]) is nn.Linear
+
+
+# ---------------------------------------------------------------- C ABI
+
+def _declared_symbols() -> list[str]:
+    text = (ROOT / "include" / "diffucore_amd.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert _declared_symbols() == sorted(_lib.SYMBOLS)
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built (run __graft_entry__.build())")
+def test_library_exports_every_declared_symbol():
+    so = _lib.lib()
+    assert so is not None, _lib.load_error()
+    for name in _declared_symbols():
+        assert hasattr(so, name), name
+    assert so.dc_abi_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
+def test_argument_checks_fail_before_any_launch():
+    """Invalid arguments are rejected on the host, with a message, before any
+    HIP call (so these run without a GPU)."""
+    so = _lib.lib()
+    assert so.dc_quantize_rows(None, _lib.BF16, 4, 300, 300, 256, None, 300, None, None) == 1
+    assert b"group" in so.dc_last_error() or b"null" in so.dc_last_error()
+    assert so.dc_quantize_rows(1, _lib.BF16, 4, 512, 512, 3, 1, 512, 1, None) == 1
+    assert b"group" in so.dc_last_error()
+    assert so.dc_quantize_rows(1, _lib.BF16, 0, 512, 512, 0, 1, 512, 1, None) == 0      # empty batch
+    assert so.dc_w8a8_gemm(16, 24, 16, 24, 16, 16, None, -1, 16, _lib.BF16, 8, 4, 8, 24, None) == 2
+    assert b"K" in so.dc_last_error()
+    assert so.dc_w8a8_gemm(16, 32, 16, 32, 16, 16, None, 7, 16, _lib.BF16, 8, 4, 8, 32, None) == 1
+    assert so.dc_int8_attn_workspace_bytes(1, 24, 4608, 4608, 128) > 24 * 4608 * 128
+    assert so.dc_int8_attn_workspace_bytes(1, 1, 1, 1, 200) == 0
+    st = (_lib.ctypes.c_int64 * 3)(8, 8, 8)
+    assert so.dc_int8_attn_fwd(16, 16, 16, 16, _lib.BF16, 1, 1, 4, 4, 36, st, st, st, st, 0.1, 16, 1 << 20,
+                               None) == 2
+    assert b"head dim" in so.dc_last_error()
+    assert so.dc_int8_attn_fwd(16, 16, 16, 16, _lib.F32, 1, 1, 4, 4, 64, st, st, st, st, 0.1, 16, 1 << 20,
+                               None) == 1
+
+
+def test_bench_refuses_more_than_one_gpu():
+    res = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 2 and "one GPU" in res.stderr
