@@ -25,6 +25,9 @@ FLAGS = [
     "-ffp-contract=off",
     # no packed-fp32 VALU instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # register-staged tile arrays stay in registers: never let the backend
+    # move a private array into spare LDS (it adds an LDS round trip per tile)
+    "-mllvm", "-disable-promote-alloca-to-lds",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <type_traits>
 
 #include "../../include/diffucore_amd.h"
 
@@ -95,6 +96,29 @@ template <int DT>
 __device__ __forceinline__ float round_to(float x) {
   if constexpr (DT == DC_F32) return x;
   else return h16_to_f32<DT>(f32_to_h16<DT>(x));
+}
+
+// ---------------------------------------------------------------- compile-time loops
+
+// static_for<N>(f) calls f(std::integral_constant<int, i>{}) for i = 0 .. N-1.
+// Array indices inside f are constants from the start, so small register
+// arrays are promoted to registers before loop unrolling would run.
+template <int I, int N>
+struct StaticFor {
+  template <class F>
+  __device__ __forceinline__ static void run(F& f) {
+    f(std::integral_constant<int, I>{});
+    StaticFor<I + 1, N>::run(f);
+  }
+};
+template <int N>
+struct StaticFor<N, N> {
+  template <class F>
+  __device__ __forceinline__ static void run(F&) {}
+};
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  StaticFor<0, N>::run(f);
 }
 
 // ---------------------------------------------------------------- wave reductions

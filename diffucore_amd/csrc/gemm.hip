@@ -21,7 +21,6 @@
 // deals workgroups round-robin over them) works a contiguous, L2-friendly range.
 #include "common.h"
 
-#include <cstdlib>
 
 namespace dc {
 
@@ -125,34 +124,38 @@ __global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
 #define GEMM_LOAD(kt_)                                                                                   \
   {                                                                                                      \
     const int k0_ = (kt_) * BK;                                                                          \
-    _Pragma("unroll") for (int u = 0; u < NWL; ++u) {                                                    \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+    static_for<NWL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
       const int n = min(n0 + r, p.N - 1), k = k0_ + 16 * c;                                              \
       wst[u] = *reinterpret_cast<const uint4*>(p.w + (int64_t)n * p.ldw + min((int64_t)k, kmax));        \
-    }                                                                                                    \
-    _Pragma("unroll") for (int u = 0; u < NAL; ++u) {                                                    \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+    });                                                                                                  \
+    static_for<NAL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
       const int m = min(m0 + r, p.M - 1), k = k0_ + 16 * c;                                              \
       ast[u] = *reinterpret_cast<const uint4*>(p.a + (int64_t)m * p.lda + min((int64_t)k, kmax));        \
-    }                                                                                                    \
+    });                                                                                                  \
   }
 #define GEMM_STORE(stage_, kt_)                                                                          \
   {                                                                                                      \
     uint8_t* base_ = smem + (stage_) * STAGE;                                                            \
-    _Pragma("unroll") for (int u = 0; u < NWL; ++u) {                                                    \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+    static_for<NWL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
       const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
       const uint4 v_ = wst[u];                                                                           \
       *reinterpret_cast<uint4*>(base_ + r * PITCH + c * 16) =                                            \
           make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
-    }                                                                                                    \
-    _Pragma("unroll") for (int u = 0; u < NAL; ++u) {                                                    \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                            \
+    });                                                                                                  \
+    static_for<NAL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
       const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
       const uint4 v_ = ast[u];                                                                           \
       *reinterpret_cast<uint4*>(base_ + BN * PITCH + r * PITCH + c * 16) =                               \
           make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
-    }                                                                                                    \
+    });                                                                                                  \
   }
 #define GEMM_FRAGS(buf_, stage_, ks_)                                                                    \
   {                                                                                                      \
@@ -322,8 +325,6 @@ template <int OUT_DT, int BIAS_DT>
 static int pick_tile(GemmArgs p, hipStream_t st) {
   // 256 x 256 tiles while they fill the device; smaller tiles for small problems
   const int64_t big = (int64_t)((p.N + 255) / 256) * ((p.M + 255) / 256);
-  static const int cfg = getenv("DC_GEMM_CFG") ? atoi(getenv("DC_GEMM_CFG")) : 0;
-  if (cfg == 1) return launch_gemm<Tile<2, 2, 4, 4>, OUT_DT, BIAS_DT>(p, st);
   if (big >= 192) return launch_gemm<Tile<2, 4, 4, 2>, OUT_DT, BIAS_DT>(p, st);
   return launch_gemm<Tile<2, 2, 2, 2>, OUT_DT, BIAS_DT>(p, st);
 }
