@@ -9,8 +9,13 @@ linear2). Every linear is a W8A8 ``Int8Linear`` with its own random weights
 ``attention_bhld(..., "int8_turing")``. Algorithmic work is 74.36 TOP per
 step (GEMM 2*M*N*K, attention 4*B*H*S^2*D). Inputs are resident in HBM.
 
+The timed steps carry HIP events around every kernel call (on torch's current
+stream, where the kernels run), so the same region gives the per-kernel
+times: GEMM, attention, quantize, and ``gemm_big``, the 256 x 256-tile GEMM
+launches with M >= 4096 whose roofline is reported (algorithmic 2*M*N*K ops
+and M*K + N*K + 2*M*N + scale/bias bytes per launch, over the average launch).
+
 The same run also measures, and adds to the JSON line:
-  * per-kernel rooflines from HIP events (GEMM, attention, quantize);
   * the full synthetic FLUX-schnell denoise step (flux_step.py) with INT8
     attention + W8A8 linears against the same step with bf16 SDPA and bf16
     linears, ms per step and the final-latent deviation after 4 steps;
@@ -18,6 +23,7 @@ The same run also measures, and adds to the JSON line:
     row sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--no-full] [--no-cpu]
+    python bench.py --copy-calibration   # 1 GiB device copy for counter scaling
 """
 
 from __future__ import annotations
@@ -89,21 +95,20 @@ class HotPath:
         self.total_ops = sum(op[3] for op in self.ops)
         self.ws = None
 
-    def run(self):
-        from diffucore_amd import attention_bhld
-        q, k, v = self.qkv
-        for kind, layer, x, _ in self.ops:
-            if kind == "gemm":
-                layer(x)
-            else:
-                attention_bhld(q, k, v, "int8_turing")
-
-    def attribute(self):
-        """One pass with HIP events around every kernel call (torch's current
-        stream, where the kernels run): time and work per kernel kind."""
+    def run(self, recs=None):
+        """One step. With ``recs`` (a list), HIP events on torch's current
+        stream (where every kernel of this package is launched) bracket each
+        quantize, GEMM and attention call and are appended as
+        ``(kind, start, end, ops, bytes, big)``."""
         from diffucore_amd import _int8, attention_bhld
         q, k, v = self.qkv
-        recs = []
+        if recs is None:
+            for kind, layer, x, _ in self.ops:
+                if kind == "gemm":
+                    layer.matmul_quantized(*_int8.quantize_activation(x, layer.group), x.dtype)
+                else:
+                    attention_bhld(q, k, v, "int8_turing")
+            return
         for kind, layer, x, ops in self.ops:
             if kind == "gemm":
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
@@ -113,23 +118,30 @@ class HotPath:
                 layer.matmul_quantized(qx, sx, x.dtype)
                 e2.record()
                 qbytes = x.numel() * x.element_size() + x.numel() + 4 * x.shape[0]
-                recs.append(("quant", e0, e1, 0, qbytes))
-                recs.append(("gemm", e1, e2, ops, 0))
+                M, K, N = x.shape[0], x.shape[1], layer.out_features
+                gbytes = M * K + N * K + 4 * (M + N) + (2 * N) + 2 * M * N
+                recs.append(("quant", e0, e1, 0, qbytes, False))
+                recs.append(("gemm", e1, e2, ops, gbytes, M >= 4096))
             else:
                 e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
                 e0.record()
                 attention_bhld(q, k, v, "int8_turing")
                 e1.record()
-                recs.append(("attn", e0, e1, ops, 0))
-        torch.cuda.synchronize()
-        out = {}
-        for kind, a, b, ops, nbytes in recs:
-            d = out.setdefault(kind, {"ms": 0.0, "ops": 0, "bytes": 0, "launches": 0})
+                recs.append(("attn", e0, e1, ops, 0, False))
+
+
+def summarize(recs):
+    """Per-kernel totals over recorded events; ``gemm_big`` is the subset of
+    GEMM launches with M >= 4096 (the 256 x 256-tile kernel)."""
+    out = {}
+    for kind, a, b, ops, nbytes, big in recs:
+        for key in (kind, "gemm_big") if big else (kind,):
+            d = out.setdefault(key, {"ms": 0.0, "ops": 0, "bytes": 0, "launches": 0})
             d["ms"] += a.elapsed_time(b)
             d["ops"] += ops
             d["bytes"] += nbytes
             d["launches"] += 1
-        return out
+    return out
 
 
 def time_steps(fn, steps, warmup):
@@ -143,6 +155,17 @@ def time_steps(fn, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def copy_calibration(mib: int = 1024, reps: int = 5):
+    """A plain device copy of ``mib`` MiB, ``reps`` times: the known-size
+    kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.ones(mib << 18, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_each_way": mib << 20, "reps": reps}), flush=True)
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -205,11 +228,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-full", action="store_true", help="skip the full FLUX step vs bf16 comparison")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (scales the rocprofv3 byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
               "run it with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import flux_step as FS
     from diffucore_amd import _lib, quantize_linears, set_attention_backend
@@ -250,31 +278,48 @@ def main():
 
     hp = HotPath(model, shape, dev)
     log(f"hot path: {len(hp.ops)} calls, {hp.total_ops / 1e12:.2f} TOP per step; timing {args.steps} steps")
+    recs = []
     with torch.no_grad():
-        ms = time_steps(hp.run, args.steps, args.warmup)
-        attr = hp.attribute()
+        for _ in range(args.warmup):
+            hp.run()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            hp.run(recs)
+        t1.record()
+        torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    attr = summarize(recs)
     tops = hp.total_ops / (ms * 1e-3) / 1e12
     log(f"hot path: {ms:.3f} ms/step, {tops:.1f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% of int8 peak)")
 
     kernels = {}
     for kind, d in attr.items():
+        per = {"ms_per_step": round(d["ms"] / args.steps, 3), "launches_per_step": d["launches"] // args.steps,
+               "avg_launch_us": round(1e3 * d["ms"] / d["launches"], 2)}
         if d["ops"]:
-            kernels[kind] = {"ms": round(d["ms"], 3), "launches": d["launches"],
-                             "TOPS": round(d["ops"] / (d["ms"] * 1e-3) / 1e12, 1)}
-        else:
-            kernels[kind] = {"ms": round(d["ms"], 3), "launches": d["launches"],
-                             "GBps": round(d["bytes"] / (d["ms"] * 1e-3) / 1e9, 1)}
-    g = attr["gemm"]
-    achieved = g["ops"] / g["launches"] / (g["ms"] / g["launches"] * 1e-3) / 1e12
+            per["TOPS"] = round(d["ops"] / (d["ms"] * 1e-3) / 1e12, 1)
+        if d["bytes"]:
+            per["GBps"] = round(d["bytes"] / (d["ms"] * 1e-3) / 1e9, 1)
+        kernels[kind] = per
+    g = attr["gemm_big"]
+    ops_per_launch = g["ops"] / g["launches"]
+    bytes_per_launch = g["bytes"] / g["launches"]
+    launch_s = g["ms"] / g["launches"] * 1e-3
+    achieved = ops_per_launch / launch_s / 1e12
     traffic = None
     tfile = ROOT / "profiles" / "gemm_flux_step_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-    roofline = {"kernel": "w8a8_gemm_kernel (all FLUX-step launches)", "bound": "mfma",
-                "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+    roofline = {"kernel": "w8a8_gemm_kernel<Tile<2,4,4,2>> (256x256 tiles): the 152 FLUX-step launches with "
+                          "M >= 4096 (img qkv/proj/mlp, single linear1/linear2)",
+                "bound": "mfma", "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                 "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": traffic,
-                "algorithmic_ops_per_launch": g["ops"] // g["launches"],
-                "avg_launch_us": round(1e3 * g["ms"] / g["launches"], 2)}
+                "algorithmic_ops_per_launch": int(ops_per_launch),
+                "algorithmic_bytes_per_launch": int(bytes_per_launch),
+                "avg_launch_us": round(1e6 * launch_s, 2),
+                "launches_timed": g["launches"]}
 
     result = {
         "metric": METRIC, "value": round(tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
