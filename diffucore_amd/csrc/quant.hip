@@ -5,9 +5,15 @@
 //   scale = max(amax / 127, 1e-30),  q = clamp(rint(x / scale), -128, 127)
 // with an IEEE float32 division (bit-exact with _quantize_rows, _int8.py:87-97).
 //
-// Layout: one workgroup per row. Each lane owns chunks of 8 consecutive
-// elements (one 16-byte load for 16-bit inputs). HBM-bound: a row is read
-// once, held in registers, reduced to its absmax and written as int8.
+// A row is read once, held in registers, reduced to its absmax and written as
+// int8. A 256-element group goes to 8 lanes (one 16-byte load per lane per 64
+// elements for 16-bit inputs). Rows of 1, 2, 4 or 8 groups fill 8 to 64 lanes
+// and reduce inside the wave; other rows are packed back to back into
+// workgroups and reduce segment maxima through LDS. The loads of a lane are
+// all issued before any is used, and the many short wave tasks let late loads
+// overlap early arithmetic. The arithmetic per element (rotation, absmax,
+// code) is about 20 VALU instructions: at FLUX shapes the kernel is bound by
+// VALU issue and the HBM stream together.
 //
 // ConvRot (group 256): x @ H_256 with H_256 = H4 (x) H4 (x) H4 (x) H4 / 16.
 // The in-group index i = 64*d1 + 16*d2 + 4*d3 + d4 is split so that the
@@ -17,28 +23,10 @@
 //   d3  - lane bit 2 (ds_swizzle xor 4) and the chunk's upper/lower half
 //   d4  - within 4 consecutive elements (in registers)
 // Each H4 step is y[j] = S - 2*x[3-j] with S = (x0 + x1) + (x2 + x3), applied
-// along d1, d2, d3, d4 in that order, then scaled by 1/16 (exact).
+// along d1, d2, d3, d4 in that order; the result is scaled by 1/16 (exact).
 #include "common.h"
 
 namespace dc {
-
-template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t off, float (&f)[8]) {
-  if constexpr (DT == DC_F32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
-    const float4 a = p[0], b = p[1];
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-  } else {
-    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = h16_to_f32<DT>(w[i] & 0xffffu);
-      f[2 * i + 1] = h16_to_f32<DT>(w[i] >> 16);
-    }
-  }
-}
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -49,13 +37,17 @@ __device__ __forceinline__ float swz_xor4(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x101F));
 }
 
-// y[j] = S - 2*x[3-j], S = (x0 + x1) + (x2 + x3)
+// y[j] = S - 2*x[3-j], S = (x0 + x1) + (x2 + x3). 2*x is exact, so the fused
+// multiply-add rounds exactly like the subtraction it replaces.
+__device__ __forceinline__ float s_minus_2x(float s, float x) { return __builtin_fmaf(-2.0f, x, s); }
+
 __device__ __forceinline__ void h4(float& x0, float& x1, float& x2, float& x3) {
   const float s = (x0 + x1) + (x2 + x3);
-  const float y0 = s - 2.0f * x3, y1 = s - 2.0f * x2, y2 = s - 2.0f * x1, y3 = s - 2.0f * x0;
+  const float y0 = s_minus_2x(s, x3), y1 = s_minus_2x(s, x2), y2 = s_minus_2x(s, x1), y3 = s_minus_2x(s, x0);
   x0 = y0; x1 = y1; x2 = y2; x3 = y3;
 }
 
+// 16 * (x @ H_256) of the lane's 256-group, in place.
 // v[j][e]: element 64*j + 8*q8 + e of the lane's 256-group, q8 = 2*d2 + d3hi,
 // with d2 = lane & 3 and d3hi = (lane >> 2) & 1.
 __device__ __forceinline__ void hadamard256(float (&v)[4][8]) {
@@ -70,7 +62,7 @@ __device__ __forceinline__ void hadamard256(float (&v)[4][8]) {
       const float x = v[j][e];
       const float pair = x + dpp<0xB1>(x);
       const float s = pair + dpp<0x4E>(pair);
-      v[j][e] = s - 2.0f * dpp<0x1B>(x);
+      v[j][e] = s_minus_2x(s, dpp<0x1B>(x));
     }
   // d3 = 2*d3hi + (e >> 2): partner lane l^4 holds the other d3hi
 #pragma unroll
@@ -81,8 +73,8 @@ __device__ __forceinline__ void hadamard256(float (&v)[4][8]) {
       const float pair = xa + xb;
       const float s = pair + swz_xor4(pair);
       const float ra = swz_xor4(xa), rb = swz_xor4(xb);
-      v[j][e] = s - 2.0f * rb;
-      v[j][e + 4] = s - 2.0f * ra;
+      v[j][e] = s_minus_2x(s, rb);
+      v[j][e + 4] = s_minus_2x(s, ra);
     }
   // d4: within 4 consecutive elements
 #pragma unroll
@@ -90,10 +82,239 @@ __device__ __forceinline__ void hadamard256(float (&v)[4][8]) {
     h4(v[j][0], v[j][1], v[j][2], v[j][3]);
     h4(v[j][4], v[j][5], v[j][6], v[j][7]);
   }
+  // (the factor 1/16 is applied by the caller)
+}
+
+// ---------------------------------------------------------------- int8 codes
+//
+// The reference's code is clamp(rint(fl(x / s)), -128, 127) with an IEEE
+// division. Here every |x| <= amax and s >= fl(amax / 127), so |x / s| <=
+// 127 (1 + 2^-23) and the clamp never acts. With inv = fl(1 / s) (once per
+// row), the exact product u = x * inv and fl(x / s) both lie within
+// |x / s| * 2^-24 of x / s. fma(x, inv, 1.5 * 2^23) rounds u to an integer n
+// (ties to even), its low byte being the two's complement code, and
+// fma(x, inv, -n) gives u - n to within 2^-26. Unless u lies within
+// (|n| + 1) * 2^-22 - 2^-24 (> |u - fl(x / s)|) of a half-integer, u and
+// fl(x / s) round to the same integer. A lane holding an element inside that
+// window (about 1e-5 of random elements) redoes its codes with the division.
+//
+// After the rotation the values still carry the butterfly's factor 16: the
+// kernels fold the exact 1/16 into amax and inv (a power-of-two scaling is
+// exact above 2^-122; below, the code is 0 either way) and apply it to x only
+// on the division path.
+constexpr float QMAGIC = 12582912.0f;              // 1.5 * 2^23
+constexpr float NEAR_HALF = 0.49999976158142090f;  // 0.5 - 2^-22
+constexpr float NEAR_SLOPE = 2.384185791015625e-07f;  // 2^-22
+
+__device__ __forceinline__ uint32_t code_fast(float x, float inv, bool& near) {
+  const float y = __builtin_fmaf(x, inv, QMAGIC);
+  const float n = y - QMAGIC;
+  near |= __builtin_fmaf(fabsf(n), NEAR_SLOPE, fabsf(__builtin_fmaf(x, inv, -n))) >= NEAR_HALF;
+  return __float_as_uint(y);
+}
+
+__device__ __forceinline__ uint32_t code_exact(float x, float s) {
+  return (uint32_t)(int)fminf(fmaxf(rintf(x / s), -128.0f), 127.0f);
+}
+
+// low bytes of a, b, c, d -> one word
+__device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
+// Codes of NG groups of 4 chunks (8 elements each) held by one lane, stored at
+// qrow + off[n][j] for the valid chunks. The values are PRE times the ones to
+// quantize (PRE = 16 after the rotation, else 1); s is the row's scale.
+template <int NG, int PRE>
+__device__ __forceinline__ void quantize_store(const float (&v)[NG][4][8], const bool (&ok)[NG][4],
+                                               const int (&off)[NG][4], float s, int8_t* qrow) {
+  constexpr float unpre = 1.0f / PRE;
+  const float inv = (1.0f / s) * unpre;
+  bool near = false;
+  uint32_t w[NG][4][2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int n = 0; n < NG; ++n)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[j][e] *= 0.0625f;
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float* e = &v[n][j][4 * h];
+        const uint32_t a = code_fast(e[0], inv, near), b = code_fast(e[1], inv, near);
+        const uint32_t c = code_fast(e[2], inv, near), d = code_fast(e[3], inv, near);
+        w[n][j][h] = pack4(a, b, c, d);
+      }
+#pragma unroll
+  for (int n = 0; n < NG; ++n)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (ok[n][j]) *reinterpret_cast<uint2*>(qrow + off[n][j]) = make_uint2(w[n][j][0], w[n][j][1]);
+  // Rare: redo this lane's codes with the division and store them again. The
+  // stores keep the compiler from evaluating the divisions unconditionally.
+  if (near) {
+#pragma unroll
+    for (int n = 0; n < NG; ++n)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float* e = &v[n][j][0];
+        const uint32_t lo = pack4(code_exact(e[0] * unpre, s), code_exact(e[1] * unpre, s),
+                                  code_exact(e[2] * unpre, s), code_exact(e[3] * unpre, s));
+        const uint32_t hi = pack4(code_exact(e[4] * unpre, s), code_exact(e[5] * unpre, s),
+                                  code_exact(e[6] * unpre, s), code_exact(e[7] * unpre, s));
+        if (ok[n][j]) *reinterpret_cast<uint2*>(qrow + off[n][j]) = make_uint2(lo, hi);
+      }
+  }
+}
+
+// scale = max(amax / 127, 1e-30) from the absmax of PRE-scaled values
+template <int PRE>
+__device__ __forceinline__ float row_scale(float amax_pre) {
+  return fmaxf((amax_pre * (1.0f / PRE)) / 127.0f, 1e-30f);
+}
+
+// ---------------------------------------------------------------- vector kernels
+//
+// Element layout (both kernels): a lane owns, in each 256-element group it
+// covers, the 4 chunks 64*j + 8*q8 (j = 0..3) with q8 = ((r & 3) << 1) | (r >> 2),
+// r = lane & 7; 8 lanes cover a group. Each chunk is one 16-byte load for
+// 16-bit inputs. Needs K % 8 == 0 and 16-byte aligned rows; ROT needs K % 256 == 0.
+
+// 8 elements from 16 (16-bit types) or 32 (float32) raw bytes
+template <int DT>
+__device__ __forceinline__ void unpack8(const uint4 (&r)[DT == DC_F32 ? 2 : 1], bool ok, float (&f)[8]) {
+  if constexpr (DT == DC_F32) {
+    const uint32_t w[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = __uint_as_float(ok ? w[i] : 0u);
+  } else {
+    const uint32_t w[4] = {ok ? r[0].x : 0u, ok ? r[0].y : 0u, ok ? r[0].z : 0u, ok ? r[0].w : 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = h16_to_f32<DT>(w[i] & 0xffffu);
+      f[2 * i + 1] = h16_to_f32<DT>(w[i] >> 16);
+    }
+  }
+}
+
+// Group g0 + units * n (n < NG) of the row for the lane's unit g0 < units.
+// Every load is issued, unconditionally, before any is used: chunks past the
+// row (or of idle lanes) read the row's first chunk and are zeroed after.
+template <int DT, int NG>
+__device__ __forceinline__ void load_groups(const void* x, int64_t rowoff, int K, int g0, int units, int q8,
+                                            float (&v)[NG][4][8], bool (&ok)[NG][4], int (&off)[NG][4]) {
+  constexpr int NQ = DT == DC_F32 ? 2 : 1;
+  uint4 raw[NG][4][NQ];
+#pragma unroll
+  for (int n = 0; n < NG; ++n)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      off[n][j] = 256 * (g0 + units * n) + 64 * j + 8 * q8;
+      ok[n][j] = g0 < units && off[n][j] < K;
+      const int64_t o = rowoff + (ok[n][j] ? off[n][j] : 0);
+      const uint4* p = DT == DC_F32 ? reinterpret_cast<const uint4*>(static_cast<const float*>(x) + o)
+                                    : reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + o);
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) raw[n][j][h] = p[h];
+    }
+#pragma unroll
+  for (int n = 0; n < NG; ++n)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) unpack8<DT>(raw[n][j], ok[n][j], v[n][j]);
+}
+
+template <int NG>
+__device__ __forceinline__ float lane_amax(const float (&v)[NG][4][8]) {
+  float a = 0.0f;
+#pragma unroll
+  for (int n = 0; n < NG; ++n)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(v[n][j][e]));
+  return a;
+}
+
+// max over the SEG lanes of an aligned segment (SEG = 8 .. 64)
+template <int SEG>
+__device__ __forceinline__ float seg_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, swz_xor4(v));
+  if constexpr (SEG >= 16) v = fmaxf(v, __shfl_xor(v, 8));
+  if constexpr (SEG >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (SEG >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Rows of up to 24 groups: SEG lanes per row (256 / SEG rows per workgroup),
+// NG groups per lane; the row maximum is a cross-lane reduction inside the
+// wave (no LDS, no barrier).
+template <int DT, int SEG, int NG, bool ROT>
+__global__ void __launch_bounds__(256) quant_seg_kernel(const void* __restrict__ x, int64_t ldx, int K, int64_t M,
+                                                        int8_t* __restrict__ q, int64_t ldq,
+                                                        float* __restrict__ scale) {
+  constexpr int RPB = 256 / SEG;
+  const int t = threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * RPB + t / SEG;
+  if (row >= M) return;  // a segment leaves as a whole; nothing below synchronizes
+  const int li = t % SEG, r = li & 7;
+  const int q8 = ((r & 3) << 1) | (r >> 2);
+  float v[NG][4][8];
+  bool ok[NG][4];
+  int off[NG][4];
+  load_groups<DT, NG>(x, row * ldx, K, li >> 3, SEG / 8, q8, v, ok, off);
+  if constexpr (ROT) {
+#pragma unroll
+    for (int n = 0; n < NG; ++n) hadamard256(v[n]);
+  }
+  constexpr int PRE = ROT ? 16 : 1;
+  const float s = row_scale<PRE>(seg_max<SEG>(lane_amax(v)));
+  quantize_store<NG, PRE>(v, ok, off, s, q + row * ldq);
+  if (li == 0) scale[row] = s;
+}
+
+// One 256-group per 8 lanes, RPB rows per workgroup (8 * G lanes each, rows
+// back to back). The row maximum is reduced inside each S-lane segment
+// (S = 8 * gcd(G, 8), so no segment straddles two rows), then over the row's
+// G * 8 / S segment maxima in LDS. Rows past M run with their loads zeroed and
+// their stores skipped, so every lane reaches the barrier.
+template <int DT, int S, bool ROT>
+__global__ void __launch_bounds__(1024) quant_rows_lds_kernel(const void* __restrict__ x, int64_t ldx, int K, int64_t M,
+                                                              int rpb, float inv_lr, int8_t* __restrict__ q,
+                                                              int64_t ldq, float* __restrict__ scale) {
+  __shared__ float red[128];
+  const int t = threadIdx.x, r = t & 7;
+  const int G = K >> 8, lr = 8 * G;
+  // t / lr: (t + 0.5) / lr is at least 0.5 / lr from an integer, far above
+  // the float error for t, lr <= 1024
+  const int rloc = (int)(((float)t + 0.5f) * inv_lr), li = t - rloc * lr;
+  const int64_t row = (int64_t)blockIdx.x * rpb + rloc;
+  const bool live = rloc < rpb && row < M;
+  const int q8 = ((r & 3) << 1) | (r >> 2);
+  float v[1][4][8];
+  bool ok[1][4];
+  int off[1][4];
+  load_groups<DT, 1>(x, (live ? row : 0) * ldx, K, li >> 3, live ? G : 0, q8, v, ok, off);
+  if constexpr (ROT) hadamard256(v[0]);
+  const float seg = seg_max<S>(lane_amax(v));
+  if ((t & (S - 1)) == 0) red[t / S] = seg;
+  __syncthreads();
+  if (!live) return;
+  const int nseg = lr / S, s0 = rloc * nseg;
+  float amax = red[s0];
+  for (int i = 1; i < nseg; ++i) amax = fmaxf(amax, red[s0 + i]);
+  constexpr int PRE = ROT ? 16 : 1;
+  const float sc = row_scale<PRE>(amax);
+  quantize_store<1, PRE>(v, ok, off, sc, q + row * ldq);
+  if (li == 0) scale[row] = sc;
+}
+
+// Generic path (group 0, any K, any alignment): two passes over the row.
+template <int DT>
+__device__ __forceinline__ float load1(const void* base, int64_t i) {
+  if constexpr (DT == DC_F32) return static_cast<const float*>(base)[i];
+  else return h16_to_f32<DT>(static_cast<const uint16_t*>(base)[i]);
 }
 
 __device__ __forceinline__ float block_max(float v, float* red) {
@@ -107,79 +328,6 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return r;
 }
 
-__device__ __forceinline__ uint32_t code4(float a, float b, float c, float d, float s) {
-  // IEEE division then round-half-even, clamp to [-128, 127]
-  const float qa = fminf(fmaxf(rintf(a / s), -128.0f), 127.0f);
-  const float qb = fminf(fmaxf(rintf(b / s), -128.0f), 127.0f);
-  const float qc = fminf(fmaxf(rintf(c / s), -128.0f), 127.0f);
-  const float qd = fminf(fmaxf(rintf(d / s), -128.0f), 127.0f);
-  return ((uint32_t)(uint8_t)(int8_t)(int)qa) | ((uint32_t)(uint8_t)(int8_t)(int)qb << 8) |
-         ((uint32_t)(uint8_t)(int8_t)(int)qc << 16) | ((uint32_t)(uint8_t)(int8_t)(int)qd << 24);
-}
-
-// Vector path: K % 8 == 0, 16-byte aligned rows. NJ chunks of 8 per lane.
-template <int DT, int NJ, bool ROT>
-__global__ void __launch_bounds__(1024) quant_rows_kernel(const void* __restrict__ x, int64_t ldx, int K,
-                                                          int8_t* __restrict__ q, int64_t ldq,
-                                                          float* __restrict__ scale) {
-  __shared__ float red[16];
-  const int64_t row = blockIdx.x;
-  const int t = threadIdx.x, nt = blockDim.x;
-  int off[NJ];
-  bool ok[NJ];
-  if constexpr (ROT) {
-    static_assert(NJ == 4, "the rotation layout owns 4 chunks per lane");
-    const int g = t >> 3, r = t & 7;
-    const int q8 = ((r & 3) << 1) | (r >> 2);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      off[j] = 256 * g + 64 * j + 8 * q8;
-      ok[j] = 256 * g < K;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      off[j] = 8 * (t + j * nt);
-      ok[j] = off[j] < K;
-    }
-  }
-  float v[NJ][8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    if (ok[j]) {
-      load8<DT>(x, row * ldx + off[j], v[j]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
-    }
-  }
-  if constexpr (ROT) hadamard256(v);
-#pragma unroll
-  for (int j = 0; j < NJ; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[j][e]));
-  amax = block_max(amax, red);
-  const float s = fmaxf(amax / 127.0f, 1e-30f);
-  int8_t* qrow = q + row * ldq;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    if (!ok[j]) continue;
-    uint2 out;
-    out.x = code4(v[j][0], v[j][1], v[j][2], v[j][3], s);
-    out.y = code4(v[j][4], v[j][5], v[j][6], v[j][7], s);
-    *reinterpret_cast<uint2*>(qrow + off[j]) = out;
-  }
-  if (t == 0) scale[row] = s;
-}
-
-// Generic path (group 0, any K, any alignment): two passes over the row.
-template <int DT>
-__device__ __forceinline__ float load1(const void* base, int64_t i) {
-  if constexpr (DT == DC_F32) return static_cast<const float*>(base)[i];
-  else return h16_to_f32<DT>(static_cast<const uint16_t*>(base)[i]);
-}
-
 template <int DT>
 __global__ void __launch_bounds__(256) quant_rows_generic(const void* __restrict__ x, int64_t ldx, int64_t K,
                                                           int8_t* __restrict__ q, int64_t ldq,
@@ -190,11 +338,64 @@ __global__ void __launch_bounds__(256) quant_rows_generic(const void* __restrict
   for (int64_t i = threadIdx.x; i < K; i += blockDim.x) amax = fmaxf(amax, fabsf(load1<DT>(x, row * ldx + i)));
   amax = block_max(amax, red);
   const float s = fmaxf(amax / 127.0f, 1e-30f);
-  for (int64_t i = threadIdx.x; i < K; i += blockDim.x) {
-    const float v = fminf(fmaxf(rintf(load1<DT>(x, row * ldx + i) / s), -128.0f), 127.0f);
-    q[row * ldq + i] = (int8_t)(int)v;
-  }
+  for (int64_t i = threadIdx.x; i < K; i += blockDim.x) q[row * ldq + i] = (int8_t)code_exact(load1<DT>(x, row * ldx + i), s);
   if (threadIdx.x == 0) scale[row] = s;
+}
+
+template <int DT, int SEG, int NG, bool ROT>
+static int launch_seg(const void* x, int64_t M, int K, int64_t ldx, int8_t* q, int64_t ldq, float* scale,
+                      hipStream_t st) {
+  constexpr int RPB = 256 / SEG;
+  hipLaunchKernelGGL((quant_seg_kernel<DT, SEG, NG, ROT>), dim3((unsigned)((M + RPB - 1) / RPB)), dim3(256), 0, st,
+                     x, ldx, K, M, q, ldq, scale);
+  return launch_status("quant_seg_kernel");
+}
+
+template <int DT, bool ROT>
+static int launch_seg_cfg(int seg, const void* x, int64_t M, int K, int64_t ldx, int8_t* q, int64_t ldq, float* scale,
+                          hipStream_t st) {
+  switch (seg) {
+    case 8: return launch_seg<DT, 8, 1, ROT>(x, M, K, ldx, q, ldq, scale, st);
+    case 16: return launch_seg<DT, 16, 1, ROT>(x, M, K, ldx, q, ldq, scale, st);
+    case 32: return launch_seg<DT, 32, 1, ROT>(x, M, K, ldx, q, ldq, scale, st);
+    default: return launch_seg<DT, 64, 1, ROT>(x, M, K, ldx, q, ldq, scale, st);
+  }
+}
+
+template <int DT, int S, bool ROT>
+static int launch_lds(const void* x, int64_t M, int K, int64_t ldx, int8_t* q, int64_t ldq, float* scale,
+                      hipStream_t st) {
+  const int G = K / 256, lr = 8 * G;
+  int rpb = 8 / (S / 8);                      // rows per workgroup that fill whole waves
+  while (rpb > 1 && rpb * lr > 1024) rpb /= 2;
+  const int nt = (rpb * lr + 63) / 64 * 64;
+  hipLaunchKernelGGL((quant_rows_lds_kernel<DT, S, ROT>), dim3((unsigned)((M + rpb - 1) / rpb)), dim3(nt), 0, st, x,
+                     ldx, K, M, rpb, 1.0f / (float)lr, q, ldq, scale);
+  return launch_status("quant_rows_lds_kernel");
+}
+
+// Kernel choice: one 256-group per 8 lanes. Rows of 1, 2, 4 or 8 groups fill
+// 8 to 64 lanes and reduce inside the wave; other lengths (multiples of 256,
+// up to 128 groups) pack rows into workgroups and combine segment maxima in
+// LDS. Many small wave tasks let the loads of late waves overlap the
+// arithmetic of early ones.
+template <int DT, bool ROT>
+static int launch_vec(const void* x, int64_t M, int K, int64_t ldx, int8_t* q, int64_t ldq, float* scale,
+                      hipStream_t st) {
+  const int G = (K + 255) / 256;
+  if (G == 1 || G == 2 || G == 4 || G == 8 || K % 256) {
+    if (G <= 8) return launch_seg_cfg<DT, ROT>(G <= 1 ? 8 : G <= 2 ? 16 : G <= 4 ? 32 : 64, x, M, K, ldx, q, ldq,
+                                               scale, st);
+  }
+  if (K % 256 == 0 && G <= 128) {
+    switch (G % 8 == 0 ? 64 : G % 4 == 0 ? 32 : G % 2 == 0 ? 16 : 8) {
+      case 64: return launch_lds<DT, 64, ROT>(x, M, K, ldx, q, ldq, scale, st);
+      case 32: return launch_lds<DT, 32, ROT>(x, M, K, ldx, q, ldq, scale, st);
+      case 16: return launch_lds<DT, 16, ROT>(x, M, K, ldx, q, ldq, scale, st);
+      default: return launch_lds<DT, 8, ROT>(x, M, K, ldx, q, ldq, scale, st);
+    }
+  }
+  return DC_EUNSUPPORTED;  // the caller takes the generic kernel
 }
 
 template <int DT>
@@ -205,30 +406,14 @@ static int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, int gr
                    ((reinterpret_cast<uintptr_t>(q) & 7) == 0) && (ldq % 8 == 0) && K <= 32768;
   if (group) {
     if (!vec) return fail(DC_EUNSUPPORTED, "dc_quantize_rows: the rotation needs 16-byte aligned rows and K <= 32768");
-    const int nt = (int)(((K / 32) + 63) / 64 * 64);
-    hipLaunchKernelGGL((quant_rows_kernel<DT, 4, true>), dim3((unsigned)M), dim3(nt), 0, st, x, ldx, (int)K, q, ldq,
-                       scale);
-    return launch_status("quant_rows_kernel<rot>");
+    return launch_vec<DT, true>(x, M, (int)K, ldx, q, ldq, scale, st);
   }
-  if (!vec) {
-    hipLaunchKernelGGL((quant_rows_generic<DT>), dim3((unsigned)M), dim3(256), 0, st, x, ldx, K, q, ldq, scale);
-    return launch_status("quant_rows_generic");
+  if (vec) {
+    const int rc = launch_vec<DT, false>(x, M, (int)K, ldx, q, ldq, scale, st);
+    if (rc != DC_EUNSUPPORTED) return rc;
   }
-  const int64_t nch = K / 8;
-  if (nch <= 256) {
-    const int nt = (int)((nch + 63) / 64 * 64);
-    hipLaunchKernelGGL((quant_rows_kernel<DT, 1, false>), dim3((unsigned)M), dim3(nt), 0, st, x, ldx, (int)K, q,
-                       ldq, scale);
-  } else if (nch <= 2048) {
-    const int nt = (int)(((nch + 1) / 2 + 63) / 64 * 64);
-    hipLaunchKernelGGL((quant_rows_kernel<DT, 2, false>), dim3((unsigned)M), dim3(nt), 0, st, x, ldx, (int)K, q,
-                       ldq, scale);
-  } else {
-    const int nt = (int)(((nch + 3) / 4 + 63) / 64 * 64);
-    hipLaunchKernelGGL((quant_rows_kernel<DT, 4, false>), dim3((unsigned)M), dim3(nt), 0, st, x, ldx, (int)K, q,
-                       ldq, scale);
-  }
-  return launch_status("quant_rows_kernel");
+  hipLaunchKernelGGL((quant_rows_generic<DT>), dim3((unsigned)M), dim3(256), 0, st, x, ldx, K, q, ldq, scale);
+  return launch_status("quant_rows_generic");
 }
 
 }  // namespace dc

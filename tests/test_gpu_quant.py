@@ -58,15 +58,94 @@ def test_codes_bit_exact_convrot(gpu, M, K, dtype):
     assert diff.max() <= 1 and (diff != 0).mean() < 1e-2
 
 
-def test_zero_rows_and_strided_input(gpu):
+# shapes that select each kernel configuration: rows of 1/2/4/8 groups of 256
+# reduced inside the wave (8-64 lanes), other multiples of 256 packed several
+# rows per workgroup with 8/16/32/64-lane segment maxima combined in LDS (with
+# batches that leave the last workgroup part-empty), up to 128 groups per row;
+# rows that are not a multiple of 256 (short ones in the wave kernel, long
+# ones in the generic kernel)
+CONFIG_SHAPES = [
+    (333, 768, 256, torch.bfloat16), (1000, 1280, 0, torch.float16), (999, 1536, 256, torch.float16),
+    (777, 3072, 0, torch.bfloat16), (300, 5120, 256, torch.float16), (129, 12288, 0, torch.bfloat16),
+    (65, 15360, 256, torch.float32), (3, 32512, 256, torch.bfloat16), (5, 32768, 0, torch.float16),
+    (64, 2304, 0, torch.float16), (50, 2600, 0, torch.bfloat16), (100, 700, 0, torch.float16),
+    (4097, 512, 256, torch.bfloat16), (4097, 1024, 0, torch.float16), (1025, 2048, 256, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("M,K,group,dtype", CONFIG_SHAPES)
+def test_every_kernel_configuration(gpu, M, K, group, dtype):
+    x = _x(M, K, dtype, seed=M ^ K, outliers=0.005)
+    q, s = _int8.quantize_activation(x.to(gpu), group)
+    q_ref, s_ref = OQ.quantize_activation(np32(x), group)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("col0", [48, 44])   # 16-byte aligned rows (vector kernel) / not (generic kernel)
+def test_zero_rows_and_strided_input(gpu, col0):
     x = torch.randn(16, 600, dtype=torch.float16)
     x[3] = 0
-    xs = x[:, 44:556]                     # ldx = 600, K = 512, 16-byte aligned rows
-    q, s = _int8.quantize_activation(xs.to(gpu), 0)
-    q_ref, s_ref = OQ.quantize_rows(np32(xs))
+    xd = x.to(gpu)
+    xs = xd[:, col0:col0 + 512]           # ldx = 600, K = 512
+    q, s = _int8.quantize_activation(xs, 0)
+    q_ref, s_ref = OQ.quantize_rows(np32(x[:, col0:col0 + 512]))
     assert np.array_equal(q.cpu().numpy(), q_ref)
     assert np.array_equal(s.cpu().numpy(), s_ref)
     assert s[3].item() == np.float32(1e-30) and (q[3] == 0).all()
+
+
+def _steps(x: np.ndarray, k: np.ndarray) -> np.ndarray:
+    """x moved by k float32 ulps (k in -2..2)."""
+    out = x.copy()
+    for _ in range(2):
+        up, dn = k > 0, k < 0
+        out[up] = np.nextafter(out[up], np.float32(np.inf))
+        out[dn] = np.nextafter(out[dn], np.float32(-np.inf))
+        k = k - np.sign(k)
+    return out
+
+
+@pytest.mark.parametrize("K", [256, 1280, 3072, 15360])
+def test_codes_at_and_around_ties(gpu, K):
+    """Quotients x / s on half-integers and 1-2 ulps either side, where a
+    reciprocal-based rounding would part from rint(x / s): element 0 of each
+    row fixes amax, the others are fl(h * s) for half-integers h, nudged."""
+    rng = np.random.default_rng(K)
+    rows = 64
+    x = np.zeros((rows, K), np.float32)
+    for r in range(rows):
+        amax = np.float32(rng.uniform(0.25, 8.0)) if r else np.float32(15.875)   # row 0: s = 1/8 exactly
+        s = np.float32(amax / np.float32(127.0))
+        h = (rng.integers(-127, 127, K - 1) + 0.5).astype(np.float32)
+        xr = (h * s).astype(np.float32)
+        if r % 2:
+            xr = _steps(xr, rng.integers(-2, 3, K - 1))
+        x[r, 0], x[r, 1:] = amax, np.clip(xr, -amax, amax)
+    q, sc = _int8.quantize_activation(torch.from_numpy(x).to(gpu), 0)
+    q_ref, s_ref = OQ.quantize_rows(x)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("K", [256, 3072, 12288])
+def test_rotated_codes_at_exact_ties(gpu, K):
+    """Inputs whose rotation is exact and lands on m / 16 with max 254 / 16,
+    so s = 1/8 and every odd m is a tie m / 2 (ties to even): x = z H / 16 for
+    integer z, which the butterfly inverts exactly."""
+    rng = np.random.default_rng(K)
+    G = K // 256
+    z = rng.integers(-20, 21, (8, K)).astype(np.float64)
+    z[:, ::256] = 254                       # the max of every row: 254 / 16
+    H = OQ.hadamard(256).astype(np.float64) * 16          # +-1 entries
+    x = (z.reshape(8, G, 256) @ H / 256).reshape(8, K).astype(np.float32)
+    y = OQ.rotate_butterfly(x, 256)
+    assert np.array_equal(y, (z / 16).astype(np.float32))   # the rotation is exact here
+    q, sc = _int8.quantize_activation(torch.from_numpy(x).to(gpu), 256)
+    q_ref, s_ref = OQ.quantize_activation(x, 256)
+    assert (s_ref == np.float32(0.125)).all()
+    assert np.array_equal(sc.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
 
 
 def test_empty_batch(gpu):

@@ -216,3 +216,16 @@ def test_bench_refuses_more_than_one_gpu():
     res = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                          timeout=120)
     assert res.returncode == 2 and "one GPU" in res.stderr
+
+
+def test_quantize_row_index_formula():
+    """The LDS quantize kernel finds a lane's row as int((t + 0.5) * fl(1 / lr))
+    (float32) instead of t / lr: exact for every row width it launches
+    (lr = 8 * G lanes, G = 1..128 groups of 256) and every lane t < 1024."""
+    import numpy as np
+    t = np.arange(1024, dtype=np.float32)
+    for G in range(1, 129):
+        lr = 8 * G
+        inv = np.float32(1.0) / np.float32(lr)
+        r = ((t + np.float32(0.5)) * inv).astype(np.float32).astype(np.int64)
+        assert np.array_equal(r, np.arange(1024) // lr), lr
