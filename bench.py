@@ -24,6 +24,7 @@ The same run also measures, and adds to the JSON line:
 
     python bench.py [--steps K] [--warmup W] [--no-full] [--no-cpu]
     python bench.py --copy-calibration   # 1 GiB device copy for counter scaling
+    python bench.py --shapes             # per-shape report for every BASELINE config
 """
 
 from __future__ import annotations
@@ -219,6 +220,124 @@ def cpu_baseline(shape, budget_s: float = 12.0, rows: int = 256):
     }
 
 
+# ---------------------------------------------------------------- per-shape report
+
+ATTN_SHAPES = [
+    # name, B, H, Sq, Skv, D, dtype, per-channel K offset std (UNet recipe) or 0
+    ("sd15_self", 2, 8, 4096, 4096, 40, torch.float16, 2.0),
+    ("sd15_cross", 2, 8, 4096, 77, 40, torch.float16, 2.0),
+    ("sdxl_self_4096", 2, 10, 4096, 4096, 64, torch.float16, 2.0),
+    ("sdxl_self_1024", 2, 20, 1024, 1024, 64, torch.float16, 2.0),
+    ("sdxl_cross_4096", 2, 10, 4096, 77, 64, torch.float16, 2.0),
+    ("sdxl_cross_1024", 2, 20, 1024, 77, 64, torch.float16, 2.0),
+    ("flux_joint", 1, 24, 4608, 4608, 128, torch.bfloat16, 0.0),
+]
+
+LIN_SHAPES = [
+    # name, M, K, N, dtype (activations and output)
+    ("sd15_ff", 8192, 320, 1280, torch.float32),
+    ("sdxl_qkvo_4096", 8192, 640, 640, torch.float16),
+    ("sdxl_qkvo_1024", 2048, 1280, 1280, torch.float16),
+    ("sdxl_cross_kv_640", 154, 2048, 640, torch.float16),
+    ("sdxl_cross_kv_1280", 154, 2048, 1280, torch.float16),
+    ("sdxl_geglu_4096", 8192, 640, 5120, torch.float16),
+    ("sdxl_ffout_4096", 8192, 2560, 640, torch.float16),
+    ("sdxl_geglu_1024", 2048, 1280, 10240, torch.float16),
+    ("sdxl_ffout_1024", 2048, 5120, 1280, torch.float16),
+    ("flux_img_qkv", 4096, 3072, 9216, torch.bfloat16),
+    ("flux_img_proj", 4096, 3072, 3072, torch.bfloat16),
+    ("flux_img_mlp_up", 4096, 3072, 12288, torch.bfloat16),
+    ("flux_img_mlp_down", 4096, 12288, 3072, torch.bfloat16),
+    ("flux_txt_qkv", 512, 3072, 9216, torch.bfloat16),
+    ("flux_txt_mlp_down", 512, 12288, 3072, torch.bfloat16),
+    ("flux_single_linear1", 4608, 3072, 21504, torch.bfloat16),
+    ("flux_single_linear2", 4608, 15360, 3072, torch.bfloat16),
+]
+
+
+def per_call_ms(fn, reps: int = 20) -> float:
+    """Median of ``reps`` calls, each bracketed by HIP events on the current stream."""
+    for _ in range(3):
+        fn()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in ev)
+    return t[reps // 2]
+
+
+def _cmp(y, ref):
+    a, b = y.float().flatten(), ref.float().flatten()
+    return {"max_abs": float((a - b).abs().max()), "rel_l2": float((a - b).norm() / b.norm()),
+            "cos": float(a @ b / (a.norm() * b.norm()))}
+
+
+def shapes_report(dev):
+    """One JSON line per BASELINE config shape: time, TOPS, % of peak, accuracy."""
+    import torch.nn.functional as F
+    from diffucore_amd import Int8Linear, attention_bhld, quantize_activation
+    mixed_peak = 2.0 / (1.0 / INT8_PEAK_TOPS + 1.0 / 2500.0)
+    g = torch.Generator(device=dev)
+    for name, B, H, S, Skv, D, dt, koff in ATTN_SHAPES:
+        g.manual_seed(0)
+        # the UNet recipe: [B, S, H*D] tensors viewed (B, H, S, D) without a copy
+        q = torch.randn(B, S, H * D, generator=g, device=dev).to(dt).view(B, S, H, D).transpose(1, 2)
+        k = torch.randn(B, Skv, H, D, generator=g, device=dev)
+        if koff:
+            k = k + torch.randn(H, D, generator=g, device=dev) * koff
+        k = k.to(dt).reshape(B, Skv, H * D).view(B, Skv, H, D).transpose(1, 2)
+        v = torch.randn(B, Skv, H * D, generator=g, device=dev).to(dt).view(B, Skv, H, D).transpose(1, 2)
+        ms = per_call_ms(lambda: attention_bhld(q, k, v, "int8_turing"))
+        ms_sdpa = per_call_ms(lambda: F.scaled_dot_product_attention(q, k, v))
+        out = attention_bhld(q, k, v, "int8_turing")
+        ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(B, S, H * D)
+        ops = 4 * B * H * S * Skv * D
+        tops = ops / (ms * 1e-3) / 1e12
+        print(json.dumps({"kind": "attention", "shape": name, "B": B, "H": H, "Sq": S, "Skv": Skv, "D": D,
+                          "dtype": str(dt)[6:], "ms": round(ms, 4), "TOPS": round(tops, 1),
+                          "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
+                          "pct_mixed_ceiling": round(100 * tops / mixed_peak, 2),
+                          "sdpa_ms": round(ms_sdpa, 4), "vs_fp32_sdpa": _cmp(out, ref)}), flush=True)
+        del q, k, v, out, ref
+    for name, M, K, N, dt in LIN_SHAPES:
+        g.manual_seed(0)
+        x = torch.randn(M, K, generator=g, device=dev)
+        idx = torch.randperm(K, generator=g, device=dev)[: max(1, round(K * 0.005))]
+        x[:, idx] *= 20
+        x = x.to(dt)
+        lin = torch.nn.Linear(K, N, device=dev)
+        with torch.no_grad():
+            lin.weight.normal_(0, 0.02, generator=g)
+            lin.bias.normal_(0, 0.02, generator=g)
+        group = 256 if K % 256 == 0 else 0
+        m = Int8Linear.from_linear(lin, group)
+        if dt != torch.float32:
+            m.bias.data = m.bias.data.to(dt)
+        ms_q = per_call_ms(lambda: quantize_activation(x, group))
+        qx, sx = quantize_activation(x, group)
+        ms_g = per_call_ms(lambda: m.matmul_quantized(qx, sx, dt))
+        y = m.matmul_quantized(qx, sx, dt)
+        # the reference's unfused int8 path on the same codes: exact int32 sums
+        # (float64 holds them), then rescale's torch ops (_int8.py:322-323)
+        acc = (qx.double() @ m.weight.double().T)
+        ref = (acc.float() * (sx[:, None] * m.scale[None, :])).to(dt)
+        ref = ref + m.bias.to(dt)
+        yf = F.linear(x.float(), lin.weight.float(), lin.bias.float())
+        ops = 2 * M * N * K
+        qbytes = M * K * x.element_size() + M * K + 4 * M
+        tops = ops / (ms_g * 1e-3) / 1e12
+        print(json.dumps({"kind": "w8a8_linear", "shape": name, "M": M, "K": K, "N": N, "group": group,
+                          "dtype": str(dt)[6:], "gemm_ms": round(ms_g, 4), "TOPS": round(tops, 1),
+                          "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
+                          "quant_ms": round(ms_q, 4), "quant_GBps": round(qbytes / (ms_q * 1e-3) / 1e9, 1),
+                          "quant_pct_hbm": round(100 * qbytes / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                          "vs_int_mm_rescale": _cmp(y, ref), "vs_float_linear": _cmp(y, yf)}), flush=True)
+        del x, lin, m, qx, sx, y, acc, ref, yf
+
+
 # ---------------------------------------------------------------- main
 
 def main():
@@ -230,6 +349,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (scales the rocprofv3 byte counters) and exit")
+    ap.add_argument("--shapes", action="store_true",
+                    help="only print the per-shape report (every BASELINE config shape) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
@@ -237,6 +358,13 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.shapes:
+        from diffucore_amd import _lib
+        _lib.require()
+        torch.cuda.set_device(0)
+        with torch.no_grad():
+            shapes_report(torch.device("cuda", 0))
         return
 
     import flux_step as FS

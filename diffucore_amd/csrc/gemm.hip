@@ -8,9 +8,12 @@
 // Work split: C^T = W . A^T on v_mfma_i32_32x32x32_i8, so each lane's
 // accumulators belong to one activation row m and 4 consecutive output
 // channels n per register quad (8- or 16-byte stores in the epilogue).
-//   workgroup tile  BN x BM = (64*FN) x (64*FM), 4 waves as 2 (n) x 2 (m)
+//   workgroup tile  BN x BM = (32*WN*FN) x (32*WM*FM), WN x WM waves
 //   wave tile       (32*FN) x (32*FM) = FN x FM MFMA blocks of 32 x 32
 //   k depth         128 bytes per LDS stage, two stages
+// Two instantiations: 256 x 256 tiles on 8 waves (2 along n x 4 along m, each
+// 128 x 64) while a problem has at least 192 of them, else 128 x 128 tiles on
+// 4 waves (each 64 x 64).
 // Pipeline per 128-byte k tile (4 MFMA k-steps): operand fragments for the
 // next k-step are read from LDS while the current one's MFMAs run; the next
 // tile, staged in registers, is written to the other LDS stage after the first
@@ -20,7 +23,6 @@
 // plus an immediate. Tiles are ordered so each XCD (8 per device; the hardware
 // deals workgroups round-robin over them) works a contiguous, L2-friendly range.
 #include "common.h"
-
 
 namespace dc {
 
