@@ -11,9 +11,9 @@
 //   workgroup tile  BN x BM = (32*WN*FN) x (32*WM*FM), WN x WM waves
 //   wave tile       (32*FN) x (32*FM) = FN x FM MFMA blocks of 32 x 32
 //   k depth         128 bytes per LDS stage, two stages
-// Two instantiations: 256 x 256 tiles on 8 waves (2 along n x 4 along m, each
-// 128 x 64) while a problem has at least 192 of them, else 128 x 128 tiles on
-// 4 waves (each 64 x 64).
+// Three instantiations: 256 x 256 tiles on 8 waves (2 along n x 4 along m,
+// each 128 x 64), 192 x 256 on 8 waves (each 96 x 64) and 128 x 128 on 4 waves
+// (each 64 x 64); pick_tile chooses by how full the last round of tiles is.
 // Pipeline per 128-byte k tile (4 MFMA k-steps): operand fragments for the
 // next k-step are read from LDS while the current one's MFMAs run; the next
 // tile, staged in registers, is written to the other LDS stage after the first
@@ -323,11 +323,40 @@ static int launch_gemm(GemmArgs p, hipStream_t st) {
   return launch_status("w8a8_gemm_kernel");
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Tile shape by the fraction of the device the last round of tiles keeps busy,
+// weighted by each shape's per-tile efficiency (measured): 256 x 256 on 8
+// waves (1 per CU), 192 (n) x 256 (m) on 8 waves (1 per CU, wave tiles 96 x 64),
+// 128 x 128 on 4 waves (2 per CU). A 4096 x 9216 problem, say, is 576 tiles of
+// 256 x 256 (2.25 rounds on 256 CUs) but exactly 768 of 192 x 256.
 template <int OUT_DT, int BIAS_DT>
 static int pick_tile(GemmArgs p, hipStream_t st) {
-  // 256 x 256 tiles while they fill the device; smaller tiles for small problems
-  const int64_t big = (int64_t)((p.N + 255) / 256) * ((p.M + 255) / 256);
-  if (big >= 192) return launch_gemm<Tile<2, 4, 4, 2>, OUT_DT, BIAS_DT>(p, st);
+  struct Cand { int bn, bm, per_cu; float eff; };
+  constexpr Cand cands[3] = {{256, 256, 1, 1.0f}, {192, 256, 1, 0.95f}, {128, 128, 2, 0.7f}};
+  const int cus = device_cus();
+  int best = 0;
+  float best_score = -1.0f;
+  for (int i = 0; i < 3; ++i) {
+    const int64_t tiles = (int64_t)((p.N + cands[i].bn - 1) / cands[i].bn) * ((p.M + cands[i].bm - 1) / cands[i].bm);
+    const int64_t slots = (int64_t)cus * cands[i].per_cu;
+    const int64_t rounds = (tiles + slots - 1) / slots;
+    const float score = (float)tiles / (float)(rounds * slots) * cands[i].eff;
+    if (score > best_score) best = i, best_score = score;
+  }
+  if (best == 0) return launch_gemm<Tile<2, 4, 4, 2>, OUT_DT, BIAS_DT>(p, st);
+  if (best == 1) return launch_gemm<Tile<2, 4, 3, 2>, OUT_DT, BIAS_DT>(p, st);
   return launch_gemm<Tile<2, 2, 2, 2>, OUT_DT, BIAS_DT>(p, st);
 }
 

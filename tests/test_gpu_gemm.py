@@ -85,3 +85,23 @@ def test_short_input(gpu):
     lin = nn.Linear(256, 64, bias=False).to(gpu)
     x = torch.randn(3, 256, device=gpu)
     assert rel_l2(np32(_int8.Int8Linear.from_linear(lin)(x)), np32(lin(x))) < 0.02
+
+
+# shapes that select each tile configuration (by how full the last round of
+# tiles is): 256 x 256, 192 x 256 (with M, N and K tails), 128 x 128
+TILE_SHAPES = [(4096, 12288, 512), (4096, 3072, 512), (4000, 3000, 272), (512, 3072, 512), (4608, 3072, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", TILE_SHAPES)
+def test_every_tile_configuration(gpu, m, n, k):
+    q, w, sx, sw = _qw(m, n, k, 9)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(9)) * 0.5).to(torch.bfloat16)
+    lin = _int8.Int8Linear(k, n, bias=True, group=0, device=gpu)
+    lin.weight.copy_(w.to(gpu))
+    lin.scale_bits.copy_(sw.to(gpu).view(torch.int32))
+    lin.bias = nn.Parameter(bias.to(gpu), requires_grad=False)
+    out = lin.matmul_quantized(q.to(gpu), sx.to(gpu), torch.bfloat16)
+    ref = OG.rescale(OG.int_mm(q.numpy(), w.numpy()), sx.numpy(), sw.numpy(), np32(bias), "bf16")
+    assert np.array_equal(np32(out).view(np.uint32), ref.view(np.uint32))
+    acc = _int8.int_mm(q.to(gpu), w.to(gpu))
+    assert np.array_equal(acc.cpu().numpy(), OG.int_mm(q.numpy(), w.numpy()))
