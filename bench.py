@@ -11,9 +11,10 @@ step (GEMM 2*M*N*K, attention 4*B*H*S^2*D). Inputs are resident in HBM.
 
 The timed steps carry HIP events around every kernel call (on torch's current
 stream, where the kernels run), so the same region gives the per-kernel
-times: GEMM, attention, quantize, and ``gemm_big``, the 256 x 256-tile GEMM
-launches with M >= 4096 whose roofline is reported (algorithmic 2*M*N*K ops
-and M*K + N*K + 2*M*N + scale/bias bytes per launch, over the average launch).
+times: GEMM, attention, quantize, and GEMM per kernel plan. The roofline is
+reported for the DMA-fed 256 x 256 GEMM kernel (the largest share of the
+step): algorithmic 2*M*N*K ops and M*K + N*K + 2*M*N + scale/bias bytes per
+launch, averaged over its launches, over its average launch time.
 
 The same run also measures, and adds to the JSON line:
   * the full synthetic FLUX-schnell denoise step (flux_step.py) with INT8
@@ -94,13 +95,16 @@ class HotPath:
             self.ops.append(lin(blk.linear2, "x_h"))
         assert all(isinstance(op[1], _int8.Int8Linear) for op in self.ops if op[0] == "gemm")
         self.total_ops = sum(op[3] for op in self.ops)
+        # which GEMM kernel each linear runs (dc_w8a8_gemm_plan)
+        self.plans = [_int8.gemm_plan(op[2].shape[0], op[1].out_features, op[1].in_features)
+                      if op[0] == "gemm" else None for op in self.ops]
         self.ws = None
 
     def run(self, recs=None):
         """One step. With ``recs`` (a list), HIP events on torch's current
         stream (where every kernel of this package is launched) bracket each
         quantize, GEMM and attention call and are appended as
-        ``(kind, start, end, ops, bytes, big)``."""
+        ``(kind, start, end, ops, bytes, gemm plan or None)``."""
         from diffucore_amd import _int8, attention_bhld
         q, k, v = self.qkv
         if recs is None:
@@ -110,7 +114,7 @@ class HotPath:
                 else:
                     attention_bhld(q, k, v, "int8_turing")
             return
-        for kind, layer, x, ops in self.ops:
+        for (kind, layer, x, ops), plan in zip(self.ops, self.plans):
             if kind == "gemm":
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
                 e0.record()
@@ -121,22 +125,22 @@ class HotPath:
                 qbytes = x.numel() * x.element_size() + x.numel() + 4 * x.shape[0]
                 M, K, N = x.shape[0], x.shape[1], layer.out_features
                 gbytes = M * K + N * K + 4 * (M + N) + (2 * N) + 2 * M * N
-                recs.append(("quant", e0, e1, 0, qbytes, False))
-                recs.append(("gemm", e1, e2, ops, gbytes, M >= 4096))
+                recs.append(("quant", e0, e1, 0, qbytes, None))
+                recs.append(("gemm", e1, e2, ops, gbytes, plan))
             else:
                 e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
                 e0.record()
                 attention_bhld(q, k, v, "int8_turing")
                 e1.record()
-                recs.append(("attn", e0, e1, ops, 0, False))
+                recs.append(("attn", e0, e1, ops, 0, None))
 
 
 def summarize(recs):
-    """Per-kernel totals over recorded events; ``gemm_big`` is the subset of
-    GEMM launches with M >= 4096 (the 256 x 256-tile kernel)."""
+    """Per-kernel totals over recorded events; GEMM launches are also totalled
+    per kernel plan (``gemm_<plan>``, from dc_w8a8_gemm_plan)."""
     out = {}
-    for kind, a, b, ops, nbytes, big in recs:
-        for key in (kind, "gemm_big") if big else (kind,):
+    for kind, a, b, ops, nbytes, plan in recs:
+        for key in (kind, f"gemm_{plan}") if plan else (kind,):
             d = out.setdefault(key, {"ms": 0.0, "ops": 0, "bytes": 0, "launches": 0})
             d["ms"] += a.elapsed_time(b)
             d["ops"] += ops
@@ -431,7 +435,7 @@ def main():
         if d["bytes"]:
             per["GBps"] = round(d["bytes"] / (d["ms"] * 1e-3) / 1e9, 1)
         kernels[kind] = per
-    g = attr["gemm_big"]
+    g = attr["gemm_dma_256x256"]
     ops_per_launch = g["ops"] / g["launches"]
     bytes_per_launch = g["bytes"] / g["launches"]
     launch_s = g["ms"] / g["launches"] * 1e-3
@@ -440,8 +444,9 @@ def main():
     tfile = ROOT / "profiles" / "gemm_flux_step_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-    roofline = {"kernel": "w8a8_gemm_kernel<Tile<2,4,4,2>> (256x256 tiles): the 152 FLUX-step launches with "
-                          "M >= 4096 (img qkv/proj/mlp, single linear1/linear2)",
+    roofline = {"kernel": "w8a8_gemm_dma_kernel (256x256 tiles, 4 waves, operands loaded straight into LDS): the "
+                          f"{g['launches'] // args.steps} FLUX-step launches it runs (img MLP up, single linear1 "
+                          "and linear2)",
                 "bound": "mfma", "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                 "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": traffic,
                 "algorithmic_ops_per_launch": int(ops_per_launch),

@@ -14,6 +14,8 @@
 // Three instantiations: 256 x 256 tiles on 8 waves (2 along n x 4 along m,
 // each 128 x 64), 192 x 256 on 8 waves (each 96 x 64) and 128 x 128 on 4 waves
 // (each 64 x 64); pick_tile chooses by how full the last round of tiles is.
+// 256 x 256 tiles with K % 256 == 0 go to w8a8_gemm_dma_kernel instead (4
+// waves of 128 x 128, operands loaded straight into LDS; described there).
 // Pipeline per 128-byte k tile (4 MFMA k-steps): operand fragments for the
 // next k-step are read from LDS while the current one's MFMAs run; the next
 // tile, staged in registers, is written to the other LDS stage after the first
@@ -72,174 +74,37 @@ __device__ __forceinline__ void store1(void* out, int64_t idx, float y) {
 }
 
 // Tile configuration: WN x WM waves, each owning FN x FM MFMA blocks of 32 x 32.
-template <int WN_, int WM_, int FN_, int FM_>
+// WN x WM waves, each FN x FM MFMA blocks of 32 x 32; RB register tiles of
+// global loads in flight (tile kt + 1 + RB is fetched during iteration kt)
+template <int WN_, int WM_, int FN_, int FM_, int RB_>
 struct Tile {
-  static constexpr int WN = WN_, WM = WM_, FN = FN_, FM = FM_;
+  static constexpr int WN = WN_, WM = WM_, FN = FN_, FM = FM_, RB = RB_;
   static constexpr int NT = 64 * WN * WM;               // threads
   static constexpr int BN = 32 * WN * FN, BM = 32 * WM * FM;
   static constexpr int LDS = 2 * (BN + BM) * PITCH + (2 * BN + BM) * 4;
 };
 
-template <class T, int OUT_DT, int BIAS_DT>
-__global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
-  constexpr int FN = T::FN, FM = T::FM, NT = T::NT;
-  constexpr int BN = T::BN, BM = T::BM;
-  constexpr int CPR = BK / 16;                    // 16-byte chunks per row
-  constexpr int NWL = BN * CPR / NT, NAL = BM * CPR / NT;
-  static_assert(BN * CPR % NT == 0 && BM * CPR % NT == 0, "tile must split evenly over the threads");
-  constexpr int STAGE = (BN + BM) * PITCH;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-
-  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int l32 = lane & 31, hf = lane >> 5;
-
-  // tile order: XCD-contiguous ranges, then GROUP_M m-tiles per n sweep
+// Tile order: XCD-contiguous ranges of workgroups (the hardware deals them
+// round-robin over the 8 XCDs), then GROUP_M m-tiles per sweep along n.
+__device__ __forceinline__ void tile_origin(const GemmArgs& p, int BM, int BN, int& m0, int& n0) {
   const int nwg = gridDim.x, wg = blockIdx.x;
   const int logical = (nwg % 8 == 0) ? (wg % 8) * (nwg / 8) + wg / 8 : wg;
   const int per_group = GROUP_M * p.tiles_n;
   const int grp = logical / per_group;
   const int first_m = grp * GROUP_M;
   const int gsize = min(p.tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (logical % per_group) % gsize;
-  const int tn = (logical % per_group) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
+  m0 = (first_m + (logical % per_group) % gsize) * BM;
+  n0 = ((logical % per_group) / gsize) * BN;
+}
 
-  const int wn = wv % T::WN, wm = wv / T::WN;
-  // per-lane fragment bases: row (wave base + l32), byte 16 hf; + 32 i rows, + 32 ks bytes
-  const int wfrag = (wn * 32 * FN + l32) * PITCH + 16 * hf;
-  const int afrag = BN * PITCH + (wm * 32 * FM + l32) * PITCH + 16 * hf;
-
-  v16i acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j) acc[i][j] = v16i{0};
-
-  uint4 wst[NWL], ast[NAL];
-  v4i wf[2][FN], af[2][FM];
-  const int nk = (p.K + BK - 1) / BK;
-
-  // Row indices are clamped into range (rows past M or N only feed outputs that
-  // are never stored) and chunks past K are zeroed by a mask when they are
-  // stored to LDS, so the loads carry no branches and no waits.
-  const int64_t kmax = p.K - 16;
-#define GEMM_LOAD(kt_)                                                                                   \
-  {                                                                                                      \
-    const int k0_ = (kt_) * BK;                                                                          \
-    static_for<NWL>([&](auto u_) {                                                                       \
-      constexpr int u = decltype(u_)::value;                                                             \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
-      const int n = min(n0 + r, p.N - 1), k = k0_ + 16 * c;                                              \
-      wst[u] = *reinterpret_cast<const uint4*>(p.w + (int64_t)n * p.ldw + min((int64_t)k, kmax));        \
-    });                                                                                                  \
-    static_for<NAL>([&](auto u_) {                                                                       \
-      constexpr int u = decltype(u_)::value;                                                             \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
-      const int m = min(m0 + r, p.M - 1), k = k0_ + 16 * c;                                              \
-      ast[u] = *reinterpret_cast<const uint4*>(p.a + (int64_t)m * p.lda + min((int64_t)k, kmax));        \
-    });                                                                                                  \
-  }
-#define GEMM_STORE(stage_, kt_)                                                                          \
-  {                                                                                                      \
-    uint8_t* base_ = smem + (stage_) * STAGE;                                                            \
-    static_for<NWL>([&](auto u_) {                                                                       \
-      constexpr int u = decltype(u_)::value;                                                             \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
-      const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
-      const uint4 v_ = wst[u];                                                                           \
-      *reinterpret_cast<uint4*>(base_ + r * PITCH + c * 16) =                                            \
-          make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
-    });                                                                                                  \
-    static_for<NAL>([&](auto u_) {                                                                       \
-      constexpr int u = decltype(u_)::value;                                                             \
-      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
-      const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
-      const uint4 v_ = ast[u];                                                                           \
-      *reinterpret_cast<uint4*>(base_ + BN * PITCH + r * PITCH + c * 16) =                               \
-          make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
-    });                                                                                                  \
-  }
-#define GEMM_FRAGS(buf_, stage_, ks_)                                                                    \
-  {                                                                                                      \
-    const uint8_t* base_ = smem + (stage_) * STAGE + 32 * (ks_);                                         \
-    _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                       \
-        wf[buf_][i] = *reinterpret_cast<const v4i*>(base_ + wfrag + 32 * i * PITCH);                     \
-    _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                       \
-        af[buf_][j] = *reinterpret_cast<const v4i*>(base_ + afrag + 32 * j * PITCH);                     \
-  }
-#define GEMM_MFMAS(buf_)                                                                                 \
-  _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                         \
-  _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                         \
-      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[buf_][i], af[buf_][j], acc[i][j], 0, 0, 0);
-// scheduler hints: `n` MFMAs, each followed by `per` instructions of class `mask`
-#define SCHED_INTERLEAVE(n_, mask_, per_)                                                                \
-  _Pragma("unroll") for (int z = 0; z < (n_); ++z) {                                                     \
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                   \
-    __builtin_amdgcn_sched_group_barrier((mask_), (per_), 0);                                            \
-  }                                                                                                      \
-  if constexpr ((n_) == 0) __builtin_amdgcn_sched_group_barrier((mask_), 64, 0);
-
-  constexpr int NF = FN + FM;                  // fragment reads per k-step
-  constexpr int NMF = FN * FM;                 // MFMAs per k-step
-  constexpr int NST = NWL + NAL;               // 16-byte stores / loads per thread per tile
-  constexpr int NSLOT = NMF > NF ? NMF - NF : 0;          // MFMAs left for stores / loads
-  constexpr int PER = NSLOT ? (NST + NSLOT - 1) / NSLOT : 1;
-  // this tile's output-channel scales, biases (rounded to the output dtype)
-  // and row scales, staged in LDS for the epilogue
-  float* sw_l = reinterpret_cast<float*>(smem + 2 * STAGE);
-  float* b_l = sw_l + BN;
-  float* sx_l = b_l + BN;
-  if constexpr (OUT_DT != DC_I32) {
-    for (int i = t; i < BN; i += NT) {
-      const int n = min(n0 + i, p.N - 1);
-      sw_l[i] = p.sw[n];
-      if constexpr (BIAS_DT != DC_NONE) b_l[i] = round_to<OUT_DT>(load_bias<BIAS_DT>(p.bias, n));
-    }
-    for (int i = t; i < BM; i += NT) sx_l[i] = p.sx[min(m0 + i, p.M - 1)];
-  }
-  GEMM_LOAD(0);
-  GEMM_STORE(0, 0);
-  GEMM_LOAD(1);
-  __syncthreads();
-  GEMM_FRAGS(0, 0, 0);
-  // Each k-step is its own scheduling region: its MFMAs consume fragments read
-  // one k-step earlier while it issues the reads for the next one. Barrier A
-  // (all waves stored tile kt + 1) lets k-step 3 prefetch tile kt + 1's first
-  // fragments; barrier B (all waves done reading stage cur) guards the next
-  // iteration's store into it.
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    GEMM_FRAGS(1, cur, 1);
-    GEMM_MFMAS(0);
-    GEMM_STORE(cur ^ 1, kt + 1);
-    SCHED_INTERLEAVE(NF, 0x100, 1);
-    SCHED_INTERLEAVE(NSLOT, 0x200, PER);
-    __builtin_amdgcn_sched_barrier(0);
-    GEMM_FRAGS(0, cur, 2);
-    GEMM_MFMAS(1);
-    GEMM_LOAD(kt + 2);
-    SCHED_INTERLEAVE(NF, 0x100, 1);
-    SCHED_INTERLEAVE(NSLOT, 0x020, PER);
-    __builtin_amdgcn_sched_barrier(0);
-    GEMM_FRAGS(1, cur, 3);
-    GEMM_MFMAS(0);
-    SCHED_INTERLEAVE(NF, 0x100, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();   // A
-    GEMM_FRAGS(0, cur ^ 1, 0);
-    GEMM_MFMAS(1);
-    SCHED_INTERLEAVE(NF, 0x100, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();   // B
-  }
-#undef SCHED_INTERLEAVE
-#undef GEMM_MFMAS
-#undef GEMM_LOAD
-#undef GEMM_STORE
-#undef GEMM_FRAGS
-
-  // epilogue: acc[i][j] register r -> n = n0 + nb + 32 i + 8 (r / 4) + 4 hf + r % 4, m = m0 + mb + 32 j + l32
-  const int nb = wn * 32 * FN, mb = wm * 32 * FM;
+// Stores one workgroup tile from its MFMA accumulators (C^T layout): register
+// r of acc[i][j] is output n = n0 + nb + 32 i + 8 (r / 4) + 4 hf + r % 4,
+// m = m0 + mb + 32 j + l32. sw_l / b_l / sx_l are the tile's channel scales,
+// rounded biases and row scales in LDS.
+template <int OUT_DT, int BIAS_DT, int FN, int FM>
+__device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const GemmArgs& p, int m0, int n0, int nb,
+                                           int mb, int BM, int BN, const float* sw_l, const float* b_l,
+                                           const float* sx_l, int hf, int l32) {
   const bool full = p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
@@ -287,6 +152,338 @@ __global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
   }
 }
 
+// This tile's output-channel scales, biases (rounded to the output dtype) and
+// row scales into LDS for the epilogue (threads t = 0 .. nt - 1).
+template <int OUT_DT, int BIAS_DT>
+__device__ __forceinline__ void stage_epilogue_vectors(const GemmArgs& p, int m0, int n0, int BM, int BN, int t,
+                                                       int nt, float* sw_l, float* b_l, float* sx_l) {
+  if constexpr (OUT_DT != DC_I32) {
+    for (int i = t; i < BN; i += nt) {
+      const int n = min(n0 + i, p.N - 1);
+      sw_l[i] = p.sw[n];
+      if constexpr (BIAS_DT != DC_NONE) b_l[i] = round_to<OUT_DT>(load_bias<BIAS_DT>(p.bias, n));
+    }
+    for (int i = t; i < BM; i += nt) sx_l[i] = p.sx[min(m0 + i, p.M - 1)];
+  }
+}
+
+template <class T, int OUT_DT, int BIAS_DT>
+__global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
+  constexpr int FN = T::FN, FM = T::FM, NT = T::NT;
+  constexpr int BN = T::BN, BM = T::BM;
+  constexpr int CPR = BK / 16;                    // 16-byte chunks per row
+  constexpr int NWL = BN * CPR / NT, NAL = BM * CPR / NT;
+  static_assert(BN * CPR % NT == 0 && BM * CPR % NT == 0, "tile must split evenly over the threads");
+  constexpr int STAGE = (BN + BM) * PITCH;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+
+  int m0, n0;
+  tile_origin(p, BM, BN, m0, n0);
+
+  const int wn = wv % T::WN, wm = wv / T::WN;
+  // per-lane fragment bases: row (wave base + l32), byte 16 hf; + 32 i rows, + 32 ks bytes
+  const int wfrag = (wn * 32 * FN + l32) * PITCH + 16 * hf;
+  const int afrag = BN * PITCH + (wm * 32 * FM + l32) * PITCH + 16 * hf;
+
+  v16i acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = v16i{0};
+
+  uint4 wst[T::RB][NWL], ast[T::RB][NAL];   // register tiles in flight
+  v4i wf[2][FN], af[2][FM];
+  const int nk = (p.K + BK - 1) / BK;
+
+  // Row indices are clamped into range (rows past M or N only feed outputs that
+  // are never stored) and chunks past K are zeroed by a mask when they are
+  // stored to LDS, so the loads carry no branches and no waits.
+  const int64_t kmax = p.K - 16;
+#define GEMM_LOAD(buf_, kt_)                                                                             \
+  {                                                                                                      \
+    const int k0_ = (kt_) * BK;                                                                          \
+    static_for<NWL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
+      const int n = min(n0 + r, p.N - 1), k = k0_ + 16 * c;                                              \
+      wst[buf_][u] = *reinterpret_cast<const uint4*>(p.w + (int64_t)n * p.ldw + min((int64_t)k, kmax));  \
+    });                                                                                                  \
+    static_for<NAL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
+      const int m = min(m0 + r, p.M - 1), k = k0_ + 16 * c;                                              \
+      ast[buf_][u] = *reinterpret_cast<const uint4*>(p.a + (int64_t)m * p.lda + min((int64_t)k, kmax));  \
+    });                                                                                                  \
+  }
+#define GEMM_STORE(buf_, stage_, kt_)                                                                    \
+  {                                                                                                      \
+    uint8_t* base_ = smem + (stage_) * STAGE;                                                            \
+    static_for<NWL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
+      const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
+      const uint4 v_ = wst[buf_][u];                                                                     \
+      *reinterpret_cast<uint4*>(base_ + r * PITCH + c * 16) =                                            \
+          make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
+    });                                                                                                  \
+    static_for<NAL>([&](auto u_) {                                                                       \
+      constexpr int u = decltype(u_)::value;                                                             \
+      const int ci = t + u * NT, r = ci / CPR, c = ci % CPR;                                             \
+      const uint32_t km_ = (kt_) * BK + 16 * c < p.K ? ~0u : 0u;                                         \
+      const uint4 v_ = ast[buf_][u];                                                                     \
+      *reinterpret_cast<uint4*>(base_ + BN * PITCH + r * PITCH + c * 16) =                               \
+          make_uint4(v_.x & km_, v_.y & km_, v_.z & km_, v_.w & km_);                                    \
+    });                                                                                                  \
+  }
+#define GEMM_FRAGS(buf_, stage_, ks_)                                                                    \
+  {                                                                                                      \
+    const uint8_t* base_ = smem + (stage_) * STAGE + 32 * (ks_);                                         \
+    _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                       \
+        wf[buf_][i] = *reinterpret_cast<const v4i*>(base_ + wfrag + 32 * i * PITCH);                     \
+    _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                       \
+        af[buf_][j] = *reinterpret_cast<const v4i*>(base_ + afrag + 32 * j * PITCH);                     \
+  }
+#define GEMM_MFMAS(buf_)                                                                                 \
+  _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                         \
+  _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                         \
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[buf_][i], af[buf_][j], acc[i][j], 0, 0, 0);
+// scheduler hints: `n` MFMAs, each followed by `per` instructions of class `mask`
+#define SCHED_INTERLEAVE(n_, mask_, per_)                                                                \
+  _Pragma("unroll") for (int z = 0; z < (n_); ++z) {                                                     \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                   \
+    __builtin_amdgcn_sched_group_barrier((mask_), (per_), 0);                                            \
+  }                                                                                                      \
+  if constexpr ((n_) == 0) __builtin_amdgcn_sched_group_barrier((mask_), 64, 0);
+
+  constexpr int NF = FN + FM;                  // fragment reads per k-step
+  constexpr int NMF = FN * FM;                 // MFMAs per k-step
+  constexpr int NST = NWL + NAL;               // 16-byte stores / loads per thread per tile
+  constexpr int NSLOT = NMF > NF ? NMF - NF : 0;          // MFMAs left for stores / loads
+  constexpr int PER = NSLOT ? (NST + NSLOT - 1) / NSLOT : 1;
+  // this tile's output-channel scales, biases (rounded to the output dtype)
+  // and row scales, staged in LDS for the epilogue
+  float* sw_l = reinterpret_cast<float*>(smem + 2 * STAGE);
+  float* b_l = sw_l + BN;
+  float* sx_l = b_l + BN;
+  stage_epilogue_vectors<OUT_DT, BIAS_DT>(p, m0, n0, BM, BN, t, NT, sw_l, b_l, sx_l);
+  GEMM_LOAD(0, 0);
+  GEMM_STORE(0, 0, 0);
+  static_for<T::RB>([&](auto i_) {
+    constexpr int i = decltype(i_)::value + 1;
+    GEMM_LOAD(i % T::RB, i);
+  });
+  __syncthreads();
+  GEMM_FRAGS(0, 0, 0);
+  // Each k-step is its own scheduling region: its MFMAs consume fragments read
+  // one k-step earlier while it issues the reads for the next one. Register
+  // tile (kt + 1) % RB holds tile kt + 1 (fetched RB iterations earlier): it
+  // goes to LDS stage cur ^ 1 in k-step 0 and is refilled with tile kt + 1 + RB
+  // in k-step 1. Barrier A (all waves stored tile kt + 1) lets k-step 3 prefetch
+  // tile kt + 1's first fragments; barrier B (all waves done reading stage cur)
+  // guards the next iteration's store into it. Two iterations per trip keep the
+  // register tile indices constant.
+#define GEMM_ITER(kt_, rb_)                                                                              \
+  {                                                                                                      \
+    const int cur = (kt_) & 1;                                                                           \
+    GEMM_FRAGS(1, cur, 1);                                                                               \
+    GEMM_MFMAS(0);                                                                                       \
+    GEMM_STORE(rb_, cur ^ 1, (kt_) + 1);                                                                 \
+    SCHED_INTERLEAVE(NF, 0x100, 1);                                                                      \
+    SCHED_INTERLEAVE(NSLOT, 0x200, PER);                                                                 \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    GEMM_FRAGS(0, cur, 2);                                                                               \
+    GEMM_MFMAS(1);                                                                                       \
+    GEMM_LOAD(rb_, (kt_) + 1 + T::RB);                                                                   \
+    SCHED_INTERLEAVE(NF, 0x100, 1);                                                                      \
+    SCHED_INTERLEAVE(NSLOT, 0x020, PER);                                                                 \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    GEMM_FRAGS(1, cur, 3);                                                                               \
+    GEMM_MFMAS(0);                                                                                       \
+    SCHED_INTERLEAVE(NF, 0x100, 1);                                                                      \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    __syncthreads();   /* A */                                                                           \
+    GEMM_FRAGS(0, cur ^ 1, 0);                                                                           \
+    GEMM_MFMAS(1);                                                                                       \
+    SCHED_INTERLEAVE(NF, 0x100, 1);                                                                      \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    __syncthreads();   /* B */                                                                           \
+  }
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    GEMM_ITER(kt, 1 % T::RB);
+    GEMM_ITER(kt + 1, 0);
+  }
+  if (kt < nk) GEMM_ITER(kt, 1 % T::RB);
+#undef GEMM_ITER
+#undef SCHED_INTERLEAVE
+#undef GEMM_MFMAS
+#undef GEMM_LOAD
+#undef GEMM_STORE
+#undef GEMM_FRAGS
+
+  // epilogue: acc[i][j] register r -> n = n0 + nb + 32 i + 8 (r / 4) + 4 hf + r % 4, m = m0 + mb + 32 j + l32
+  store_tile<OUT_DT, BIAS_DT, FN, FM>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l, hf, l32);
+}
+
+// ---------------------------------------------------------------- DMA-fed kernel
+//
+// 256 x 256 tiles on 4 waves (2 along n x 2 along m, each 128 x 128 = 4 x 4
+// MFMA blocks, accumulators in AGPRs, one wave per SIMD). Operands go from
+// global memory straight into LDS (global_load_lds_dwordx4: lane i of a wave
+// writes bytes 16 i .. 16 i + 15 after the wave's base) through 4 stages of 64
+// k-bytes, up to 4 stages ahead of the MFMAs, so no registers stage them. A stage is
+// W [256 rows x 64 B] then A [256 rows x 64 B], unpadded; the 16-byte chunk c
+// of row r sits at chunk c ^ ((r / 4) % 4), which spreads the 16 rows a
+// fragment read serves per cycle over all banks. One barrier per stage, half
+// way through it: every wave has waited for its own loads of the next stage
+// (vmcnt) and for its own fragment reads of the current one (lgkmcnt), so
+// after the barrier the next stage is complete and the current stage's buffer
+// is free for the loads 4 stages ahead.
+// Needs K % 256 == 0 (whole stages, 4 per trip of the unrolled loop) and
+// 256 * ldw, 256 * lda below 2^31.
+constexpr int DBK = 64;                      // k bytes per stage
+constexpr int DSTAGE = (256 + 256) * DBK;    // 32 KB
+constexpr int DMA_LOADS_PER_STAGE = 8;       // per wave: 4 KB of W + 4 KB of A
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// vmcnt(n) with the other counters left unconstrained, and vmcnt(n) together
+// with lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8)
+#define DC_WAIT_VMCNT(n_) __builtin_amdgcn_s_waitcnt(((n_) & 15) | (((n_) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define DC_WAIT_VMCNT_LGKM0(n_) __builtin_amdgcn_s_waitcnt(((n_) & 15) | (((n_) >> 4) << 14) | (7 << 4))
+
+template <int OUT_DT, int BIAS_DT>
+__global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p) {
+  constexpr int BN = 256, BM = 256, FN = 4, FM = 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t st0[DSTAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t st1[DSTAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t st2[DSTAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t st3[DSTAGE];
+  __shared__ __attribute__((aligned(16))) float epi_v[2 * BN + BM];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int wn = w & 1, wm = w >> 1;
+  int m0, n0;
+  tile_origin(p, BM, BN, m0, n0);
+
+  float* sw_l = epi_v;
+  float* b_l = epi_v + BN;
+  float* sx_l = epi_v + 2 * BN;
+  stage_epilogue_vectors<OUT_DT, BIAS_DT>(p, m0, n0, BM, BN, t, 256, sw_l, b_l, sx_l);
+  __syncthreads();
+
+  // DMA sources: wave w loads 1 KB blocks j = w + 4 u (rows 16 j .. 16 j + 15)
+  // of W and of A; lane i covers row 16 j + i / 4, logical chunk
+  // (i % 4) ^ ((i / 16) % 4) (its physical chunk is i % 4).
+  // (byte offsets from the tile's first W / A row; rows past N / M are clamped)
+  const int drow = lane >> 2, dchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const int8_t* wtile = p.w + (int64_t)n0 * p.ldw;
+  const int8_t* atile = p.a + (int64_t)m0 * p.lda;
+  uint32_t woff[4], aoff[4];   // unsigned: a scalar base plus a 32-bit lane offset
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int r = 16 * (w + 4 * u) + drow;
+    woff[u] = (uint32_t)((min(n0 + r, p.N - 1) - n0) * (int)p.ldw + 16 * dchunk);
+    aoff[u] = (uint32_t)((min(m0 + r, p.M - 1) - m0) * (int)p.lda + 16 * dchunk);
+  }
+  const int nk = p.K / DBK;   // a multiple of 4
+  // stage kt's loads; stages past the end re-read the last one (kept in bounds;
+  // their data is never used)
+#define DMA_STAGE(buf_, kt_)                                                                             \
+  {                                                                                                      \
+    const int k0_ = min((kt_), nk - 1) * DBK;                                                            \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u)                                                        \
+        __builtin_amdgcn_global_load_lds((wtile + k0_) + woff[u], (lds_void_ptr)((buf_) + 1024 * (w + 4 * u)), 16, 0, 0); \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u)                                                        \
+        __builtin_amdgcn_global_load_lds((atile + k0_) + aoff[u], (lds_void_ptr)((buf_) + 16384 + 1024 * (w + 4 * u)), 16, 0, 0); \
+  }
+
+  // fragment reads: W rows wn*128 + 32 i + l32, A rows wm*128 + 32 j + l32; k-step
+  // ks reads logical chunk 2 ks + hf, physical (2 ks + hf) ^ ((l32 / 4) % 4)
+  const int swz = (l32 >> 2) & 3;
+  const int wrow = (wn * 128 + l32) * DBK, arow = 16384 + (wm * 128 + l32) * DBK;
+  const int kc0 = 16 * (hf ^ swz), kc1 = 16 * ((2 + hf) ^ swz);
+  v16i acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = v16i{0};
+  v4i wf[2][FN], af[2][FM];
+#define DMA_FRAGS(b_, buf_, kc_)                                                                         \
+  {                                                                                                      \
+    _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                       \
+        wf[b_][i] = *reinterpret_cast<const v4i*>((buf_) + wrow + 2048 * i + (kc_));                     \
+    _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                       \
+        af[b_][j] = *reinterpret_cast<const v4i*>((buf_) + arow + 2048 * j + (kc_));                     \
+  }
+#define DMA_MFMAS(b_)                                                                                    \
+  _Pragma("unroll") for (int i = 0; i < FN; ++i)                                                         \
+  _Pragma("unroll") for (int j = 0; j < FM; ++j)                                                         \
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[b_][i], af[b_][j], acc[i][j], 0, 0, 0);
+
+  DMA_STAGE(st0, 0);
+  DMA_STAGE(st1, 1);
+  DMA_STAGE(st2, 2);
+  DMA_STAGE(st3, 3);
+  DC_WAIT_VMCNT(3 * DMA_LOADS_PER_STAGE);
+  __builtin_amdgcn_s_barrier();
+  DMA_FRAGS(0, st0, kc0);
+
+  // Iteration kt (stage buffer cur = kt % 4): k-step 0 runs on fragments read
+  // earlier while k-step 1's are read from cur; then the wave waits for its
+  // loads of stage kt + 1 and for its reads of cur, the barrier makes stage
+  // kt + 1 complete and cur free, the loads of stage kt + 4 go into cur, and
+  // k-step 1 runs while the first fragments of stage kt + 1 are read.
+#define DMA_ITER(kt_, cur_, nxt_)                                                                        \
+  {                                                                                                      \
+    DMA_FRAGS(1, cur_, kc1);                                                                             \
+    DMA_MFMAS(0);                                                                                        \
+    /* one MFMA first: its wait covers only the fragments it uses */                                     \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                   \
+    _Pragma("unroll") for (int z = 0; z < 8; ++z) {                                                      \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
+    }                                                                                                    \
+    __builtin_amdgcn_sched_group_barrier(0x008, 7, 0);                                                   \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    DC_WAIT_VMCNT_LGKM0(2 * DMA_LOADS_PER_STAGE);                                                        \
+    __builtin_amdgcn_s_barrier();                                                                        \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    DMA_STAGE(cur_, (kt_) + 4);                                                                          \
+    DMA_FRAGS(0, nxt_, kc0);                                                                             \
+    DMA_MFMAS(1);                                                                                        \
+    /* the stage's loads and the next fragment reads spread over the 16 MFMAs */                         \
+    _Pragma("unroll") for (int z = 0; z < 8; ++z) {                                                      \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                 \
+    }                                                                                                    \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+  }
+  for (int kt = 0; kt < nk; kt += 4) {
+    DMA_ITER(kt, st0, st1);
+    DMA_ITER(kt + 1, st1, st2);
+    DMA_ITER(kt + 2, st2, st3);
+    DMA_ITER(kt + 3, st3, st0);
+  }
+#undef DMA_ITER
+#undef DMA_MFMAS
+#undef DMA_FRAGS
+#undef DMA_STAGE
+  // no load may still be writing this workgroup's LDS when it ends
+  DC_WAIT_VMCNT(0);
+
+  store_tile<OUT_DT, BIAS_DT, FN, FM>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l, hf, l32);
+}
+#undef DC_WAIT_VMCNT
+#undef DC_WAIT_VMCNT_LGKM0
+
 // Rescale pass over an int32 accumulator (dc_rescale): one thread per 4 outputs.
 template <int OUT_DT, int BIAS_DT>
 __global__ void __launch_bounds__(256) rescale_kernel(const int32_t* __restrict__ acc, int64_t lda,
@@ -323,6 +520,16 @@ static int launch_gemm(GemmArgs p, hipStream_t st) {
   return launch_status("w8a8_gemm_kernel");
 }
 
+template <int OUT_DT, int BIAS_DT>
+static int launch_gemm_dma(GemmArgs p, hipStream_t st) {
+  p.tiles_n = (p.N + 255) / 256;
+  p.tiles_m = (p.M + 255) / 256;
+  const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
+  if (tiles > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm: problem too large");
+  hipLaunchKernelGGL((w8a8_gemm_dma_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)tiles), dim3(256), 0, st, p);
+  return launch_status("w8a8_gemm_dma_kernel");
+}
+
 // Compute units of the current device (cached per device).
 static int device_cus() {
   static int cus[64] = {0};
@@ -337,27 +544,42 @@ static int device_cus() {
 }
 
 // Tile shape by the fraction of the device the last round of tiles keeps busy,
-// weighted by each shape's per-tile efficiency (measured): 256 x 256 on 8
-// waves (1 per CU), 192 (n) x 256 (m) on 8 waves (1 per CU, wave tiles 96 x 64),
-// 128 x 128 on 4 waves (2 per CU). A 4096 x 9216 problem, say, is 576 tiles of
+// weighted by each shape's per-tile efficiency (measured): 256 x 256 (the
+// DMA-fed 4-wave kernel when K % 256 == 0, else 8 waves; 1 per CU),
+// 192 (n) x 256 (m) on 8 waves (1 per CU, wave tiles 96 x 64), 128 x 128 on
+// 4 waves (2 per CU). A 4096 x 9216 problem, say, is 576 tiles of
 // 256 x 256 (2.25 rounds on 256 CUs) but exactly 768 of 192 x 256.
-template <int OUT_DT, int BIAS_DT>
-static int pick_tile(GemmArgs p, hipStream_t st) {
+// Kernel plan for a problem: DC_GEMM_PLAN_* (the choice pick_tile launches).
+static int plan_tile(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
   struct Cand { int bn, bm, per_cu; float eff; };
   constexpr Cand cands[3] = {{256, 256, 1, 1.0f}, {192, 256, 1, 0.95f}, {128, 128, 2, 0.7f}};
   const int cus = device_cus();
   int best = 0;
   float best_score = -1.0f;
   for (int i = 0; i < 3; ++i) {
-    const int64_t tiles = (int64_t)((p.N + cands[i].bn - 1) / cands[i].bn) * ((p.M + cands[i].bm - 1) / cands[i].bm);
+    const int64_t tiles = ((N + cands[i].bn - 1) / cands[i].bn) * ((M + cands[i].bm - 1) / cands[i].bm);
     const int64_t slots = (int64_t)cus * cands[i].per_cu;
     const int64_t rounds = (tiles + slots - 1) / slots;
     const float score = (float)tiles / (float)(rounds * slots) * cands[i].eff;
     if (score > best_score) best = i, best_score = score;
   }
-  if (best == 0) return launch_gemm<Tile<2, 4, 4, 2>, OUT_DT, BIAS_DT>(p, st);
-  if (best == 1) return launch_gemm<Tile<2, 4, 3, 2>, OUT_DT, BIAS_DT>(p, st);
-  return launch_gemm<Tile<2, 2, 2, 2>, OUT_DT, BIAS_DT>(p, st);
+  if (best == 0) {
+    // 256 x 256 tiles: the DMA-fed kernel when its shape conditions hold
+    if (K % (4 * DBK) == 0 && 256 * lda < (int64_t(1) << 31) && 256 * ldw < (int64_t(1) << 31))
+      return DC_GEMM_PLAN_DMA_256x256;
+    return DC_GEMM_PLAN_256x256;
+  }
+  return best == 1 ? DC_GEMM_PLAN_192x256 : DC_GEMM_PLAN_128x128;
+}
+
+template <int OUT_DT, int BIAS_DT>
+static int pick_tile(GemmArgs p, hipStream_t st) {
+  switch (plan_tile(p.M, p.N, p.K, p.lda, p.ldw)) {
+    case DC_GEMM_PLAN_DMA_256x256: return launch_gemm_dma<OUT_DT, BIAS_DT>(p, st);
+    case DC_GEMM_PLAN_256x256: return launch_gemm<Tile<2, 4, 4, 2, 1>, OUT_DT, BIAS_DT>(p, st);
+    case DC_GEMM_PLAN_192x256: return launch_gemm<Tile<2, 4, 3, 2, 1>, OUT_DT, BIAS_DT>(p, st);
+    default: return launch_gemm<Tile<2, 2, 2, 2, 1>, OUT_DT, BIAS_DT>(p, st);
+  }
 }
 
 template <int OUT_DT>
@@ -395,6 +617,15 @@ static int rescale_bias(const int32_t* acc, int64_t lda, const float* sx, const 
 }  // namespace dc
 
 using namespace dc;
+
+extern "C" int dc_w8a8_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
+  clear_error();
+  if (M <= 0 || N <= 0 || K <= 0 || K % 16 || lda < K || ldw < K || lda % 16 || ldw % 16) {
+    set_error("dc_w8a8_gemm_plan: no kernel takes this shape");
+    return -1;
+  }
+  return plan_tile(M, N, K, lda, ldw);
+}
 
 extern "C" int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, const float* sx,
                             const float* sw, const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,

@@ -69,6 +69,21 @@ int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, con
                  int64_t ldo, int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
+ * Which GEMM kernel dc_w8a8_gemm runs for a problem on the current device:
+ * one of the DC_GEMM_PLAN_* codes, or -1 for a shape it rejects. Tiles are
+ * chosen by how full the last round of workgroups keeps the device. No
+ * counterpart in the reference (its GEMMs come from torch._int_mm and one
+ * CUTLASS configuration, _int8.py:200-276); for profiling and tests.
+ */
+enum {
+  DC_GEMM_PLAN_256x256 = 0,      /* 8 waves, 128 x 64 wave tiles, register-staged loads */
+  DC_GEMM_PLAN_192x256 = 1,      /* 8 waves, 96 x 64 wave tiles */
+  DC_GEMM_PLAN_128x128 = 2,      /* 4 waves, 64 x 64 wave tiles, 2 workgroups per CU */
+  DC_GEMM_PLAN_DMA_256x256 = 3   /* 4 waves, 128 x 128 wave tiles, loads straight into LDS */
+};
+int dc_w8a8_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw);
+
+/*
  * The rescale pass on an int32 accumulator, for callers that hold one.
  * Replaces rescale (src/diffucore/models/_int8.py:313-323) and the Triton
  * _rescale_kernel (_int8.py:408-417). Same rounding as dc_w8a8_gemm.

@@ -87,13 +87,19 @@ def test_short_input(gpu):
     assert rel_l2(np32(_int8.Int8Linear.from_linear(lin)(x)), np32(lin(x))) < 0.02
 
 
-# shapes that select each tile configuration (by how full the last round of
-# tiles is): 256 x 256, 192 x 256 (with M, N and K tails), 128 x 128
-TILE_SHAPES = [(4096, 12288, 512), (4096, 3072, 512), (4000, 3000, 272), (512, 3072, 512), (4608, 3072, 256)]
+# shapes that select each kernel (by how full the last round of tiles is on a
+# 256-CU device, and K % 256 for the DMA-fed 256 x 256 kernel), with M, N and
+# K tails among them
+TILE_SHAPES = [((4096, 12288, 512), "dma_256x256"), ((4608, 3072, 256), "dma_256x256"),
+               ((4096, 12288, 272), "256x256"), ((4096, 3072, 512), "192x256"),
+               ((4000, 3000, 272), "192x256"), ((512, 3072, 512), "128x128"), ((4001, 12200, 768), "dma_256x256")]
 
 
-@pytest.mark.parametrize("m,n,k", TILE_SHAPES)
-def test_every_tile_configuration(gpu, m, n, k):
+@pytest.mark.parametrize("mnk,plan", TILE_SHAPES)
+def test_every_tile_configuration(gpu, mnk, plan):
+    m, n, k = mnk
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert _int8.gemm_plan(m, n, k) == plan
     q, w, sx, sw = _qw(m, n, k, 9)
     bias = (torch.randn(n, generator=torch.Generator().manual_seed(9)) * 0.5).to(torch.bfloat16)
     lin = _int8.Int8Linear(k, n, bias=True, group=0, device=gpu)
