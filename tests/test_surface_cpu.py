@@ -229,3 +229,19 @@ def test_quantize_row_index_formula():
         inv = np.float32(1.0) / np.float32(lr)
         r = ((t + np.float32(0.5)) * inv).astype(np.float32).astype(np.int64)
         assert np.array_equal(r, np.arange(1024) // lr), lr
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
+def test_gemm_plan_choice_without_a_gpu():
+    """The GEMM tile planner runs on the host (assuming 256 CUs when no device
+    answers). FLUX-step shapes take the DMA-fed 256x256 kernel when K is a
+    multiple of 256, the 192x256 tiles when they fill the last round better,
+    and 2-per-CU 128x128 tiles for short text-token GEMMs."""
+    so = _lib.lib()
+    assert so.dc_w8a8_gemm_plan(4608, 21504, 3072, 3072, 3072) == 3      # linear1
+    assert so.dc_w8a8_gemm_plan(4608, 3072, 15360, 15360, 15360) == 3    # linear2
+    assert so.dc_w8a8_gemm_plan(4096, 9216, 3072, 3072, 3072) == 1       # image qkv
+    assert so.dc_w8a8_gemm_plan(512, 9216, 3072, 3072, 3072) == 2        # text qkv
+    assert so.dc_w8a8_gemm_plan(4096, 12288, 272, 272, 272) == 0         # K % 256 != 0
+    assert so.dc_w8a8_gemm_plan(0, 1, 16, 16, 16) == -1                  # invalid shape
+    assert [_int8.gemm_plan(4608, 21504, 3072), _int8.gemm_plan(512, 9216, 3072)] == ["dma_256x256", "128x128"]
