@@ -39,6 +39,7 @@ struct GemmArgs {
   int M, N, K;
   int tiles_m, tiles_n;
   int vec_out;  // 1 when 4-wide output stores are aligned
+  int vec16;    // 1 when 16-byte output stores at multiples of 16 bytes into a row are aligned
 };
 
 constexpr int BK = 128;            // k bytes per LDS stage
@@ -65,6 +66,33 @@ __device__ __forceinline__ float epi_pre(int acc, float sxm, float swn, float b)
   float y = round_to<OUT_DT>(materialize((float)acc * (sxm * swn)));
   if constexpr (HAS_BIAS) y = round_to<OUT_DT>(materialize(y + b));
   return y;
+}
+
+// 16-bit outputs two at a time, rounded as epi_pre rounds each (float32
+// product; round to the output type; plus the rounded bias in float32; round
+// again), with one packed conversion per rounding step.
+template <int OUT_DT>
+__device__ __forceinline__ uint32_t cvt_pair(float a, float b) {
+  const v2f x = {a, b};
+  if constexpr (OUT_DT == DC_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, v2bf));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, v2h));
+}
+template <int OUT_DT>
+__device__ __forceinline__ float pair_lo(uint32_t pk) {
+  if constexpr (OUT_DT == DC_BF16) return __uint_as_float(pk << 16);
+  else return f16_to_f32(pk & 0xffffu);
+}
+template <int OUT_DT>
+__device__ __forceinline__ float pair_hi(uint32_t pk) {
+  if constexpr (OUT_DT == DC_BF16) return __uint_as_float(pk & 0xffff0000u);
+  else return f16_to_f32(pk >> 16);
+}
+template <int OUT_DT, bool HAS_BIAS>
+__device__ __forceinline__ uint32_t epi_pair(int a0, int a1, float sxm, float s0, float s1, float b0, float b1) {
+  uint32_t pk = cvt_pair<OUT_DT>(materialize((float)a0 * (sxm * s0)), materialize((float)a1 * (sxm * s1)));
+  if constexpr (HAS_BIAS)
+    pk = cvt_pair<OUT_DT>(materialize(pair_lo<OUT_DT>(pk) + b0), materialize(pair_hi<OUT_DT>(pk) + b1));
+  return pk;
 }
 
 template <int OUT_DT>
@@ -100,56 +128,60 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& p, int BM, int BN, i
 // Stores one workgroup tile from its MFMA accumulators (C^T layout): register
 // r of acc[i][j] is output n = n0 + nb + 32 i + 8 (r / 4) + 4 hf + r % 4,
 // m = m0 + mb + 32 j + l32. sw_l / b_l / sx_l are the tile's channel scales,
-// rounded biases and row scales in LDS.
+// rounded biases and row scales in LDS; each lane reads its row scales once
+// and each group of 4 channel scales / biases once for all its rows.
 template <int OUT_DT, int BIAS_DT, int FN, int FM>
 __device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const GemmArgs& p, int m0, int n0, int nb,
                                            int mb, int BM, int BN, const float* sw_l, const float* b_l,
                                            const float* sx_l, int hf, int l32) {
+  constexpr bool HB = BIAS_DT != DC_NONE;
   const bool full = p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N;
+  float sxm[FM];
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int ml = mb + 32 * j + l32, m = m0 + ml;
-    if (!full && m >= p.M) continue;
-    float sxm = 0.0f;
-    if constexpr (OUT_DT != DC_I32) sxm = sx_l[ml];
+  for (int j = 0; j < FM; ++j) sxm[j] = OUT_DT != DC_I32 ? sx_l[mb + 32 * j + l32] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+  for (int i = 0; i < FN; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nl = nb + 32 * i + 8 * g + 4 * hf, n = n0 + nl;
+    for (int g = 0; g < 4; ++g) {
+      const int nl = nb + 32 * i + 8 * g + 4 * hf, n = n0 + nl;
+      const bool vec = full || (p.vec_out && n + 3 < p.N);
+      float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (OUT_DT != DC_I32) s4 = *reinterpret_cast<const float4*>(sw_l + nl);
+      if constexpr (HB) b4 = *reinterpret_cast<const float4*>(b_l + nl);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int m = m0 + mb + 32 * j + l32;
+        if (!full && m >= p.M) continue;
         const int64_t base = (int64_t)m * p.ldo + n;
         const int av[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
         if constexpr (OUT_DT == DC_I32) {
           int* o = static_cast<int*>(p.out);
-          if (full || (p.vec_out && n + 3 < p.N)) {
-            *reinterpret_cast<int4*>(o + base) = make_int4(av[0], av[1], av[2], av[3]);
-          } else {
-            for (int e = 0; e < 4 && n + e < p.N; ++e) o[base + e] = av[e];
-          }
-        } else {
-          const float4 s4 = *reinterpret_cast<const float4*>(sw_l + nl);
-          float4 b4 = make_float4(0.f, 0.f, 0.f, 0.f);
-          if constexpr (BIAS_DT != DC_NONE) b4 = *reinterpret_cast<const float4*>(b_l + nl);
-          constexpr bool HB = BIAS_DT != DC_NONE;
-          const float y0 = epi_pre<OUT_DT, HB>(av[0], sxm, s4.x, b4.x);
-          const float y1 = epi_pre<OUT_DT, HB>(av[1], sxm, s4.y, b4.y);
-          const float y2 = epi_pre<OUT_DT, HB>(av[2], sxm, s4.z, b4.z);
-          const float y3 = epi_pre<OUT_DT, HB>(av[3], sxm, s4.w, b4.w);
-          if (full || (p.vec_out && n + 3 < p.N)) {
-            if constexpr (OUT_DT == DC_F32) {
-              *reinterpret_cast<float4*>(static_cast<float*>(p.out) + base) = make_float4(y0, y1, y2, y3);
-            } else {
-              const uint32_t lo = f32_to_h16<OUT_DT>(y0) | (f32_to_h16<OUT_DT>(y1) << 16);
-              const uint32_t hi = f32_to_h16<OUT_DT>(y2) | (f32_to_h16<OUT_DT>(y3) << 16);
-              *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + base) = make_uint2(lo, hi);
-            }
+          if (vec) *reinterpret_cast<int4*>(o + base) = make_int4(av[0], av[1], av[2], av[3]);
+          else for (int e = 0; e < 4 && n + e < p.N; ++e) o[base + e] = av[e];
+        } else if constexpr (OUT_DT == DC_F32) {
+          const float y0 = epi_pre<OUT_DT, HB>(av[0], sxm[j], s4.x, b4.x);
+          const float y1 = epi_pre<OUT_DT, HB>(av[1], sxm[j], s4.y, b4.y);
+          const float y2 = epi_pre<OUT_DT, HB>(av[2], sxm[j], s4.z, b4.z);
+          const float y3 = epi_pre<OUT_DT, HB>(av[3], sxm[j], s4.w, b4.w);
+          if (vec) {
+            *reinterpret_cast<float4*>(static_cast<float*>(p.out) + base) = make_float4(y0, y1, y2, y3);
           } else {
             const float yv[4] = {y0, y1, y2, y3};
             for (int e = 0; e < 4 && n + e < p.N; ++e) store1<OUT_DT>(p.out, base + e, yv[e]);
           }
+        } else {
+          const uint32_t lo = epi_pair<OUT_DT, HB>(av[0], av[1], sxm[j], s4.x, s4.y, b4.x, b4.y);
+          const uint32_t hi = epi_pair<OUT_DT, HB>(av[2], av[3], sxm[j], s4.z, s4.w, b4.z, b4.w);
+          uint16_t* o16 = static_cast<uint16_t*>(p.out);
+          if (vec) {
+            *reinterpret_cast<uint2*>(o16 + base) = make_uint2(lo, hi);
+          } else {
+            const uint32_t hv[4] = {lo & 0xffffu, lo >> 16, hi & 0xffffu, hi >> 16};
+            for (int e = 0; e < 4 && n + e < p.N; ++e) o16[base + e] = (uint16_t)hv[e];
+          }
         }
       }
-  }
+    }
 }
 
 // This tile's output-channel scales, biases (rounded to the output dtype) and
@@ -164,6 +196,82 @@ __device__ __forceinline__ void stage_epilogue_vectors(const GemmArgs& p, int m0
       if constexpr (BIAS_DT != DC_NONE) b_l[i] = round_to<OUT_DT>(load_bias<BIAS_DT>(p.bias, n));
     }
     for (int i = t; i < BM; i += nt) sx_l[i] = p.sx[min(m0 + i, p.M - 1)];
+  }
+}
+
+// Epilogue of one wave's full 128 (n) x 128 (m) block through LDS: the output
+// values go to the wave's own 32 KB of LDS (`stage`, free after the main
+// loop), row m at 128 * (output bytes) per row, 16-byte chunk c of row r at
+// chunk c ^ (r % 16); then each row leaves as one contiguous run, 16 bytes per
+// lane (4 rows per store instruction for 16-bit outputs, 2 for 32-bit). The
+// MFMA layout would otherwise store 8 or 16 bytes into each of 32 rows per
+// instruction. 32-bit outputs take two passes of 64 rows. A lane reads back
+// what other lanes of its wave wrote: the wavefront fences and barrier
+// between the two halves keep the compiler from moving LDS accesses across.
+template <int OUT_DT, int BIAS_DT>
+__device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], const GemmArgs& p, int m0, int n0, int nb,
+                                               int mb, const float* sw_l, const float* b_l, const float* sx_l, int hf,
+                                               int l32, int lane, uint8_t* stage) {
+  constexpr int OB = (OUT_DT == DC_F16 || OUT_DT == DC_BF16) ? 2 : 4;
+  constexpr int ROWB = 128 * OB;   // staged row bytes
+  constexpr int CH = ROWB / 16;    // 16-byte chunks per row
+  constexpr int JP = 8 / OB;       // 32-row m blocks per pass
+  constexpr int RPI = 64 / CH;     // rows per store instruction
+  constexpr bool HB = BIAS_DT != DC_NONE;
+  float sxm[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sxm[j] = OUT_DT != DC_I32 ? sx_l[mb + 32 * j + l32] : 0.0f;
+#pragma unroll
+  for (int j0 = 0; j0 < 4; j0 += JP) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nl = nb + 32 * i + 8 * g + 4 * hf;
+        float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (OUT_DT != DC_I32) s4 = *reinterpret_cast<const float4*>(sw_l + nl);
+        if constexpr (HB) b4 = *reinterpret_cast<const float4*>(b_l + nl);
+#pragma unroll
+        for (int jj = 0; jj < JP; ++jj) {
+          const int j = j0 + jj, r = 32 * jj + l32;
+          uint8_t* row = stage + r * ROWB;
+          const int av[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          if constexpr (OUT_DT == DC_I32) {
+            const int c = 8 * i + 2 * g + hf;
+            *reinterpret_cast<int4*>(row + 16 * (c ^ (r & 15))) = make_int4(av[0], av[1], av[2], av[3]);
+          } else if constexpr (OUT_DT == DC_F32) {
+            const int c = 8 * i + 2 * g + hf;
+            const float y0 = epi_pre<OUT_DT, HB>(av[0], sxm[j], s4.x, b4.x);
+            const float y1 = epi_pre<OUT_DT, HB>(av[1], sxm[j], s4.y, b4.y);
+            const float y2 = epi_pre<OUT_DT, HB>(av[2], sxm[j], s4.z, b4.z);
+            const float y3 = epi_pre<OUT_DT, HB>(av[3], sxm[j], s4.w, b4.w);
+            *reinterpret_cast<float4*>(row + 16 * (c ^ (r & 15))) = make_float4(y0, y1, y2, y3);
+          } else {
+            const int c = 4 * i + g;
+            const uint32_t lo = epi_pair<OUT_DT, HB>(av[0], av[1], sxm[j], s4.x, s4.y, b4.x, b4.y);
+            const uint32_t hi = epi_pair<OUT_DT, HB>(av[2], av[3], sxm[j], s4.z, s4.w, b4.z, b4.w);
+            *reinterpret_cast<uint2*>(row + 16 * (c ^ (r & 15)) + 8 * hf) = make_uint2(lo, hi);
+          }
+        }
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int c = lane % CH;
+#pragma unroll
+    for (int k = 0; k < 32 * JP / RPI; ++k) {
+      const int r = RPI * k + lane / CH;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * ROWB + 16 * (c ^ (r & 15)));
+      const int64_t m = m0 + mb + 32 * j0 + r;
+      uint8_t* dst = static_cast<uint8_t*>(p.out) + (m * p.ldo + n0 + nb) * OB + 16 * c;
+      *reinterpret_cast<uint4*>(dst) = v;
+    }
+    if constexpr (JP < 4) {
+      // the next pass overwrites what this one read back
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
   }
 }
 
@@ -479,8 +587,15 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p) {
   // no load may still be writing this workgroup's LDS when it ends
   DC_WAIT_VMCNT(0);
 
-  store_tile<OUT_DT, BIAS_DT, FN, FM>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l, hf, l32);
+  if (p.vec16 && m0 + BM <= p.M && n0 + BN <= p.N) {
+    __syncthreads();   // every wave is done reading the stage buffers
+    uint8_t* stg = w == 0 ? st0 : (w == 1 ? st1 : (w == 2 ? st2 : st3));
+    store_tile_lds<OUT_DT, BIAS_DT>(acc, p, m0, n0, wn * 128, wm * 128, sw_l, b_l, sx_l, hf, l32, lane, stg);
+  } else {
+    store_tile<OUT_DT, BIAS_DT, FN, FM>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l, hf, l32);
+  }
 }
+
 #undef DC_WAIT_VMCNT
 #undef DC_WAIT_VMCNT_LGKM0
 
@@ -648,6 +763,7 @@ extern "C" int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   const int ob = elem_bytes(out_dtype);
   p.vec_out = ((reinterpret_cast<uintptr_t>(out) % (4 * (uintptr_t)(ob ? ob : 1))) == 0) && (ldo % 4 == 0) &&
               (out_dtype == DC_I32 || (reinterpret_cast<uintptr_t>(sw) & 15) == 0);
+  p.vec16 = p.vec_out && (reinterpret_cast<uintptr_t>(out) % 16) == 0 && (ldo * ob) % 16 == 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (out_dtype) {
     case DC_I32: return pick_tile<DC_I32, DC_NONE>(p, st);

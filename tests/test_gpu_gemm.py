@@ -106,8 +106,10 @@ def test_every_tile_configuration(gpu, mnk, plan):
     lin.weight.copy_(w.to(gpu))
     lin.scale_bits.copy_(sw.to(gpu).view(torch.int32))
     lin.bias = nn.Parameter(bias.to(gpu), requires_grad=False)
-    out = lin.matmul_quantized(q.to(gpu), sx.to(gpu), torch.bfloat16)
-    ref = OG.rescale(OG.int_mm(q.numpy(), w.numpy()), sx.numpy(), sw.numpy(), np32(bias), "bf16")
-    assert np.array_equal(np32(out).view(np.uint32), ref.view(np.uint32))
+    acc_ref = OG.int_mm(q.numpy(), w.numpy())
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        out = lin.matmul_quantized(q.to(gpu), sx.to(gpu), dtype)
+        ref = OG.rescale(acc_ref, sx.numpy(), sw.numpy(), np32(bias), DT[dtype])
+        assert np.array_equal(np32(out).view(np.uint32), ref.view(np.uint32)), dtype
     acc = _int8.int_mm(q.to(gpu), w.to(gpu))
-    assert np.array_equal(acc.cpu().numpy(), OG.int_mm(q.numpy(), w.numpy()))
+    assert np.array_equal(acc.cpu().numpy(), acc_ref)
