@@ -93,11 +93,24 @@ int dc_rescale(const int32_t* acc, int64_t lda, const float* sx, const float* sw
                int64_t M, int64_t N, void* stream);
 
 /*
- * Workspace size in bytes for dc_int8_attn_fwd at this shape (Lq is unused).
- * Replaces the scratch tensors fwd allocates itself
+ * Workspace size in bytes for dc_int8_attn_fwd at this shape on the current
+ * device. Replaces the scratch tensors fwd allocates itself
  * (src/diffucore/kernels/int8_attn_sm80.cu:469-476).
  */
 size_t dc_int8_attn_workspace_bytes(int B, int H, int Lq, int Lk, int D);
+
+/*
+ * How dc_int8_attn_fwd splits its work at this shape on the current device
+ * (no counterpart in the reference, whose grid is one CTA per 128-query tile,
+ * int8_attn_sm80.cu:486-494; for profiling and tests). The 128-query tiles
+ * (b, h, tile) in that order fill whole rounds of the device's resident
+ * workgroups, *dp_tiles of them, each run whole; the remaining *sk_tiles
+ * tiles' (query tile, 64-key tile) pairs are shared by *sk_blocks stream-K
+ * workgroups (0 when the last round is run whole) whose partial results a
+ * merge kernel combines. Returns 0, or DC_EINVAL for a bad shape or dtype.
+ */
+int dc_int8_attn_plan(int dtype, int B, int H, int Lq, int Lk, int D, int* dp_tiles, int* sk_blocks,
+                      int* sk_tiles);
 
 /*
  * INT8-QK / 16-bit-PV flash attention.
@@ -116,6 +129,8 @@ size_t dc_int8_attn_workspace_bytes(int B, int H, int Lq, int Lk, int D);
  *   ks    f32  [B, H, Lk64 / 64]  per-block scale amax / 127
  *   kpart f32  [B, H, ceil(Lk / 128), D]   per-window key sums
  *   ksum  f32  [B, H, D]                    per-channel key sums
+ *   part  f32  [2 * sk_blocks][128 * Dp + 256]  stream-K partial results:
+ *         unnormalized O [128][Dp], row maxima [128], row sums [128]
  */
 int dc_int8_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B,
                      int H, int Lq, int Lk, int D, const int64_t q_strides[3],

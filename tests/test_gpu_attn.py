@@ -138,3 +138,45 @@ def test_deterministic(gpu):
     q, k, v = _inputs(1, 500, 700, 3, 128, torch.bfloat16, seed=3)
     outs = [_run(q, k, v, gpu)[0] for _ in range(3)]
     assert all(torch.equal(outs[0], o) for o in outs[1:])
+
+
+def test_stream_k_pieces_match_whole_tiles(gpu):
+    """Query tiles past the last whole round of workgroups run as stream-K
+    pieces (ranges of key tiles) whose partial O, row maxima and row sums a
+    merge kernel combines. Heads run that way agree per query tile with the
+    same heads run whole (they differ only in where the running maximum sits
+    when P is rounded to bf16), and the heads run whole in both launches are
+    bit-identical."""
+    B, L, D, dtype = 1, 4096, 128, torch.bfloat16
+    H = 24
+    pl = A.attn_plan(B, H, L, L, D, dtype)
+    per_head = L // 128
+    if pl["sk_blocks"] == 0 or pl["dp_tiles"] % per_head:
+        pytest.skip(f"no stream-K split at this shape on this device: {pl}")
+    h_dp = pl["dp_tiles"] // per_head           # heads run whole in the H = 24 launch
+    n_sk = H - h_dp
+    # the stream-K heads first, then as many whole heads, as one launch run whole
+    order = list(range(h_dp, H)) + list(range(0, h_dp))[: max(0, h_dp - n_sk)]
+    order = order[:h_dp] if len(order) > h_dp else order
+    pl2 = A.attn_plan(B, len(order), L, L, D, dtype)
+    if pl2["sk_blocks"] != 0:
+        pytest.skip(f"no whole-round launch for the comparison on this device: {pl2}")
+    g = torch.Generator(device=gpu).manual_seed(11)
+    q = torch.randn(B, L, H, D, device=gpu, generator=g).to(dtype)
+    k = (torch.randn(B, L, H, D, device=gpu, generator=g) + 0.5).to(dtype)
+    v = torch.randn(B, L, H, D, device=gpu, generator=g).to(dtype)
+    out = A.int8_attention(q, k, v, D ** -0.5)
+    idx = torch.tensor(order, device=gpu)
+    out2 = A.int8_attention(q[:, :, idx].contiguous(), k[:, :, idx].contiguous(), v[:, :, idx].contiguous(), D ** -0.5)
+    for j, hh in enumerate(order):
+        if hh < h_dp:
+            assert torch.equal(out[:, :, hh], out2[:, :, j]), hh
+            continue
+        a, b_ = out[0, :, hh].float(), out2[0, :, j].float()
+        ref = F.scaled_dot_product_attention(q[:, :, hh:hh + 1].transpose(1, 2).float(),
+                                             k[:, :, hh:hh + 1].transpose(1, 2).float(),
+                                             v[:, :, hh:hh + 1].transpose(1, 2).float())[0, 0]
+        for t0 in range(0, L, 128):
+            sl = slice(t0, t0 + 128)
+            assert (a[sl] - b_[sl]).norm() / b_[sl].norm() < 5e-3, (hh, t0)
+            assert (a[sl] - ref[sl]).norm() / ref[sl].norm() < 3e-2, (hh, t0)

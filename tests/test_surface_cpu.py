@@ -245,3 +245,19 @@ def test_gemm_plan_choice_without_a_gpu():
     assert so.dc_w8a8_gemm_plan(4096, 12288, 272, 272, 272) == 0         # K % 256 != 0
     assert so.dc_w8a8_gemm_plan(0, 1, 16, 16, 16) == -1                  # invalid shape
     assert [_int8.gemm_plan(4608, 21504, 3072), _int8.gemm_plan(512, 9216, 3072)] == ["dma_256x256", "128x128"]
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
+def test_attention_work_split_without_a_gpu():
+    """The attention work split runs on the host (512 resident workgroups, 2
+    per CU on 256 CUs, when no device answers). SDXL's 640 query tiles at 4096
+    tokens run 512 whole and share the last 128 (a quarter-full round) over
+    512 stream-K workgroups; FLUX's last round (352 of 512) is full enough to
+    run whole, and so are whole rounds and short key ranges."""
+    from diffucore_amd import _attention as A
+    assert A.attn_plan(2, 10, 4096, 4096, 64, torch.float16) == {"dp_tiles": 512, "sk_blocks": 512, "sk_tiles": 128}
+    assert A.attn_plan(1, 24, 4608, 4608, 128) == {"dp_tiles": 864, "sk_blocks": 0, "sk_tiles": 0}
+    assert A.attn_plan(2, 8, 4096, 4096, 40, torch.float16) == {"dp_tiles": 512, "sk_blocks": 0, "sk_tiles": 0}
+    assert A.attn_plan(2, 10, 4096, 77, 64, torch.float16)["sk_blocks"] == 0
+    ws = _lib.lib().dc_int8_attn_workspace_bytes(2, 10, 4096, 4096, 64)
+    assert ws >= 2 * 512 * (128 * 64 + 256) * 4
