@@ -565,12 +565,16 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p) {
     DMA_STAGE(cur_, (kt_) + 4);                                                                          \
     DMA_FRAGS(0, nxt_, kc0);                                                                             \
     DMA_MFMAS(1);                                                                                        \
-    /* the stage's loads and the next fragment reads spread over the 16 MFMAs */                         \
+    /* the next fragment reads with the first 8 MFMAs (they return during the  \
+       last 8, so the next iteration's first MFMA does not wait on them), the  \
+       stage's loads with the last 8 */                                                                  \
+    _Pragma("unroll") for (int z = 0; z < 8; ++z) {                                                      \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                 \
+    }                                                                                                    \
     _Pragma("unroll") for (int z = 0; z < 8; ++z) {                                                      \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                                 \
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                 \
     }                                                                                                    \
     __builtin_amdgcn_sched_barrier(0);                                                                   \
   }

@@ -310,6 +310,77 @@ __global__ void __launch_bounds__(1024) quant_rows_lds_kernel(const void* __rest
   if (li == 0) scale[row] = sc;
 }
 
+// ---------------------------------------------------------------- activation + concatenation
+
+// GELU in float32, then rounded to the 16-bit type DT as the reference rounds
+// it (src/diffucore/models/_int8.py:433-435: 0.5 h (1 + erf(h / sqrt 2)),
+// cast to the activation dtype; the tanh form is torch's
+// gelu(approximate="tanh"), 0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))),
+// which FLUX's MLPs use).
+template <int DT>
+__device__ __forceinline__ float act_round(float x, int act) {
+  float y;
+  if (act == DC_ACT_GELU_ERF) {
+    y = (0.5f * x) * (1.0f + erff(x * 0.7071067811865476f));
+  } else {
+    const float inner = 0.7978845608028654f * (x + 0.044715f * ((x * x) * x));
+    y = (0.5f * x) * (1.0f + tanhf(inner));
+  }
+  return round_to<DT>(y);
+}
+
+// Rows of concat(x1, act(x2)): columns 0 .. K1 - 1 from x1 as they are,
+// columns K1 .. K - 1 from x2 through `act` (rounded to DT), then rotated and
+// quantized exactly like quant_rows_lds_kernel. K1 and K are multiples of 256
+// (a 256-group never straddles the two sources), so each 8-lane group unit
+// reads one source.
+template <int DT, int S, bool ROT>
+__global__ void __launch_bounds__(1024) quant_act_rows_kernel(const void* __restrict__ x1, int64_t ld1, int K1,
+                                                              const void* __restrict__ x2, int64_t ld2, int K, int act,
+                                                              int64_t M, int rpb, float inv_lr,
+                                                              int8_t* __restrict__ q, int64_t ldq,
+                                                              float* __restrict__ scale) {
+  __shared__ float red[128];
+  const int t = threadIdx.x, r = t & 7;
+  const int G = K >> 8, G1 = K1 >> 8, lr = 8 * G;
+  const int rloc = (int)(((float)t + 0.5f) * inv_lr), li = t - rloc * lr;
+  const int64_t row = (int64_t)blockIdx.x * rpb + rloc;
+  const bool live = rloc < rpb && row < M;
+  const int q8 = ((r & 3) << 1) | (r >> 2);
+  const int g = li >> 3;
+  const bool second = g >= G1;
+  const int64_t rr = live ? row : 0;
+  const void* src = second ? x2 : x1;
+  const int64_t rowoff = second ? rr * ld2 : rr * ld1;
+  float v[1][4][8];
+  bool ok[1][4];
+  int off[1][4];
+  load_groups<DT, 1>(src, rowoff, second ? K - K1 : K1, second ? g - G1 : g, live ? (second ? G - G1 : G1) : 0, q8,
+                     v, ok, off);
+  if (second) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      off[0][j] += K1;
+      if (act != DC_ACT_NONE) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[0][j][e] = act_round<DT>(v[0][j][e], act);
+      }
+    }
+  }
+  if constexpr (ROT) hadamard256(v[0]);
+  const float seg = seg_max<S>(lane_amax(v));
+  if ((t & (S - 1)) == 0) red[t / S] = seg;
+  __syncthreads();
+  if (!live) return;
+  const int nseg = lr / S, s0 = rloc * nseg;
+  float amax = red[s0];
+  for (int i = 1; i < nseg; ++i) amax = fmaxf(amax, red[s0 + i]);
+  constexpr int PRE = ROT ? 16 : 1;
+  const float sc = row_scale<PRE>(amax);
+  quantize_store<1, PRE>(v, ok, off, sc, q + row * ldq);
+  if (li == 0) scale[row] = sc;
+}
+
 // Generic path (group 0, any K, any alignment): two passes over the row.
 template <int DT>
 __device__ __forceinline__ float load1(const void* base, int64_t i) {
@@ -416,6 +487,30 @@ static int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, int gr
   return launch_status("quant_rows_generic");
 }
 
+template <int DT, int S, bool ROT>
+static int launch_act_s(const void* x1, int64_t ld1, int K1, const void* x2, int64_t ld2, int K, int act, int64_t M,
+                        int8_t* q, int64_t ldq, float* scale, hipStream_t st) {
+  const int G = K / 256, lr = 8 * G;
+  int rpb = 8 / (S / 8);
+  while (rpb > 1 && rpb * lr > 1024) rpb /= 2;
+  const int nt = (rpb * lr + 63) / 64 * 64;
+  hipLaunchKernelGGL((quant_act_rows_kernel<DT, S, ROT>), dim3((unsigned)((M + rpb - 1) / rpb)), dim3(nt), 0, st, x1,
+                     ld1, K1, x2, ld2, K, act, M, rpb, 1.0f / (float)lr, q, ldq, scale);
+  return launch_status("quant_act_rows_kernel");
+}
+
+template <int DT, bool ROT>
+static int launch_act(const void* x1, int64_t ld1, int K1, const void* x2, int64_t ld2, int K, int act, int64_t M,
+                      int8_t* q, int64_t ldq, float* scale, hipStream_t st) {
+  const int G = K / 256;
+  switch (G % 8 == 0 ? 64 : G % 4 == 0 ? 32 : G % 2 == 0 ? 16 : 8) {
+    case 64: return launch_act_s<DT, 64, ROT>(x1, ld1, K1, x2, ld2, K, act, M, q, ldq, scale, st);
+    case 32: return launch_act_s<DT, 32, ROT>(x1, ld1, K1, x2, ld2, K, act, M, q, ldq, scale, st);
+    case 16: return launch_act_s<DT, 16, ROT>(x1, ld1, K1, x2, ld2, K, act, M, q, ldq, scale, st);
+    default: return launch_act_s<DT, 8, ROT>(x1, ld1, K1, x2, ld2, K, act, M, q, ldq, scale, st);
+  }
+}
+
 }  // namespace dc
 
 using namespace dc;
@@ -436,4 +531,35 @@ extern "C" int dc_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K
     case DC_F32: return launch_quant<DC_F32>(x, M, K, ldx, group, q, ldq, scale, st);
     default: return fail(DC_EINVAL, "dc_quantize_rows: x_dtype must be DC_F16, DC_BF16 or DC_F32");
   }
+}
+
+extern "C" int dc_act_quantize_rows(const void* x1, int64_t ld1, int64_t K1, const void* x2, int64_t ld2, int64_t K2,
+                                    int act, int x_dtype, int64_t M, int group, int8_t* q, int64_t ldq, float* scale,
+                                    void* stream) {
+  clear_error();
+  const int64_t K = K1 + K2;
+  if (M < 0 || K1 < 0 || K2 < 0 || K <= 0 || ldq < K || (K1 && ld1 < K1) || (K2 && ld2 < K2))
+    return fail(DC_EINVAL, "dc_act_quantize_rows: bad M/K1/K2/ld1/ld2/ldq");
+  if (M == 0) return DC_OK;
+  if (M > 0x7fffffff) return fail(DC_EINVAL, "dc_act_quantize_rows: M too large");
+  if ((K1 && !x1) || (K2 && !x2) || !q || !scale) return fail(DC_EINVAL, "dc_act_quantize_rows: null pointer");
+  if (act != DC_ACT_NONE && act != DC_ACT_GELU_ERF && act != DC_ACT_GELU_TANH)
+    return fail(DC_EINVAL, "dc_act_quantize_rows: unknown act");
+  if (group != 0 && group != 256) return fail(DC_EINVAL, "dc_act_quantize_rows: group must be 0 or 256");
+  if (x_dtype != DC_F16 && x_dtype != DC_BF16) return fail(DC_EINVAL, "dc_act_quantize_rows: x_dtype must be DC_F16 or DC_BF16");
+  if (K1 % 256 || K2 % 256 || K > 32768)
+    return fail(DC_EUNSUPPORTED, "dc_act_quantize_rows: K1 and K2 must be multiples of 256, K1 + K2 <= 32768");
+  if ((K1 && (!aligned16(x1) || (ld1 * 2) % 16)) || (K2 && (!aligned16(x2) || (ld2 * 2) % 16)) ||
+      (reinterpret_cast<uintptr_t>(q) & 7) || ldq % 8)
+    return fail(DC_EUNSUPPORTED, "dc_act_quantize_rows: needs 16-byte aligned rows and 8-byte aligned q rows");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const void* a = K1 ? x1 : x2;
+  const int64_t la = K1 ? ld1 : ld2;
+  const void* b = K2 ? x2 : x1;
+  const int64_t lb = K2 ? ld2 : ld1;
+  if (x_dtype == DC_BF16)
+    return group ? launch_act<DC_BF16, true>(a, la, (int)K1, b, lb, (int)K, act, M, q, ldq, scale, st)
+                 : launch_act<DC_BF16, false>(a, la, (int)K1, b, lb, (int)K, act, M, q, ldq, scale, st);
+  return group ? launch_act<DC_F16, true>(a, la, (int)K1, b, lb, (int)K, act, M, q, ldq, scale, st)
+               : launch_act<DC_F16, false>(a, la, (int)K1, b, lb, (int)K, act, M, q, ldq, scale, st);
 }

@@ -51,6 +51,28 @@ int dc_abi_version(void);
 int dc_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int group,
                      int8_t* q, int64_t ldq, float* scale, void* stream);
 
+/* Activations for dc_act_quantize_rows. */
+enum { DC_ACT_NONE = 0, DC_ACT_GELU_ERF = 1, DC_ACT_GELU_TANH = 2 };
+
+/*
+ * dc_quantize_rows of the rows of concat(x1, act(x2)), in one pass:
+ *   x1 [M, K1] row stride ld1 (may be NULL with K1 == 0), taken as it is;
+ *   x2 [M, K2] row stride ld2, through act: GELU computed in float32 and
+ *   rounded to x_dtype (DC_F16 or DC_BF16), the dtype of both inputs;
+ *   q [M, K1 + K2] int8 (row stride ldq), scale [M] as dc_quantize_rows.
+ * K1 and K2 are multiples of 256, K1 + K2 <= 32768; 16-byte aligned rows.
+ * Replaces the reference's fused MLP middle, GEMM1 output -> GELU -> l2's
+ * ConvRot + quantize in one row pass (src/diffucore/models/_int8.py:326-358,
+ * 419-443: _gelu_quantize / _gelu_f16_rot_quant_kernel); act =
+ * DC_ACT_GELU_TANH covers FLUX's MLP middle (flux_dit.py:228-239) and, with
+ * x1, its single-block linear2 input cat(attention, gelu_tanh(mlp))
+ * (flux_dit.py:335), which the reference builds with torch ops before
+ * quantizing.
+ */
+int dc_act_quantize_rows(const void* x1, int64_t ld1, int64_t K1, const void* x2, int64_t ld2, int64_t K2,
+                         int act, int x_dtype, int64_t M, int group, int8_t* q, int64_t ldq, float* scale,
+                         void* stream);
+
 /*
  * W8A8 GEMM on int8 MFMA with int32 accumulation and a fused epilogue.
  *   a   [M, K] int8 (activations), row stride lda

@@ -10,11 +10,18 @@ Follows reference ``src/diffucore/models/_int8.py``:
 * ``rotate_matmul``  <- ``_rotate`` (``_int8.py:79-84``): ``t @ H`` per group.
 * ``rotate_butterfly`` <- ``_hadamard_rows`` (``_int8.py:363-372``), with the
   summation order this build fixes (see its docstring).
+* ``gelu`` / ``act_quantize`` <- the fused MLP middle ``_gelu`` and
+  ``_gelu_f16_rot_quant_kernel`` (``_int8.py:433-443``, ``_gelu_quantize``
+  ``:348-358``); the tanh form is torch's ``gelu(approximate="tanh")`` that
+  FLUX's MLPs use (``flux_dit.py:228-239, 335``).
 """
 
 from __future__ import annotations
 
 import numpy as np
+from scipy.special import erf as _erf64
+
+from .fp import round_to
 
 _H4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], np.float32)
 SCALE_FLOOR = np.float32(1e-30)
@@ -97,3 +104,35 @@ def quantize_weight(w, group: int) -> tuple[np.ndarray, np.ndarray]:
 def dequantize_weight(q, scale, group: int) -> np.ndarray:
     """``dequantize_weight`` (``_int8.py:105-107``)."""
     return rotate_matmul(np.asarray(q, np.float32) * np.asarray(scale, np.float32)[:, None], group)
+
+
+def gelu(x, approximate: str = "none", dtype: str = "bf16") -> np.ndarray:
+    """GELU of float32 ``x`` rounded to the 16-bit ``dtype`` ("bf16"/"f16"), as
+    the reference's ``_gelu`` rounds it (``_int8.py:433-435``):
+    ``(0.5 * h) * (1 + erf(h * 0.7071067811865476))``, float32 operations in
+    that order; ``approximate="tanh"``: ``(0.5 * x) * (1 + tanh(0.7978845608028654
+    * (x + 0.044715 * ((x * x) * x))))``. erf and tanh are evaluated in float64
+    and rounded once to float32. A device's float32 erf / tanh may differ from
+    that by an ulp or two; the rounding to 16 bits hides it except next to a
+    rounding boundary, so for the transcendental itself parity is within
+    tolerance, and everything after it (rotation, codes) is exact."""
+    x = np.asarray(x, np.float32)
+    if approximate == "none":
+        t = (x * np.float32(0.7071067811865476)).astype(np.float32)
+        e = _erf64(t.astype(np.float64)).astype(np.float32)
+    elif approximate == "tanh":
+        inner = (np.float32(0.7978845608028654) * (x + np.float32(0.044715) * ((x * x) * x))).astype(np.float32)
+        e = np.tanh(inner.astype(np.float64)).astype(np.float32)
+    else:
+        raise ValueError(f"unknown approximate={approximate!r}")
+    y = ((np.float32(0.5) * x) * (np.float32(1.0) + e)).astype(np.float32)
+    return round_to(y, dtype)
+
+
+def act_quantize(x2, group: int, approximate: str = "none", dtype: str = "bf16", prefix=None):
+    """``quantize_activation`` of the rows of ``cat(prefix, gelu(x2))``: what
+    the fused HIP kernel computes (prefix columns taken as they are)."""
+    h = gelu(x2, approximate, dtype)
+    if prefix is not None:
+        h = np.concatenate([np.asarray(prefix, np.float32), h], axis=-1)
+    return quantize_activation(h, group)

@@ -1,0 +1,104 @@
+"""dc_act_quantize_rows on the GPU: the fused MLP middle (GELU, then ConvRot
+and per-row int8 quantization, reference ``_int8.py:326-358, 433-443``) and
+FLUX's single-block ``cat(attention, gelu_tanh(mlp))`` input (``flux_dit.py:335``).
+
+Everything after the GELU is exact; the GELU's erf / tanh is a float32 library
+function, so the checks allow the rare element where the device's float32
+value rounds to the other neighbouring 16-bit value (parity within tolerance,
+stated in each test)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from diffucore_amd import _int8
+from oracle import quant as OQ
+from tests._util import DT, cosine, np32, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+APPROX = {"gelu": "none", "gelu_tanh": "tanh"}
+
+
+def _agree(q, s, q_ref, s_ref, code_frac=0.999):
+    """A GELU value one 16-bit ulp off (the library erf / tanh differing in the
+    last float32 bit next to a rounding boundary) moves its rotated group by
+    under one code step and the row maximum by at most that ulp: every scale
+    within 2^-8 relative, every code within 1, and at least ``code_frac`` of
+    the codes equal."""
+    q = q.cpu().numpy().astype(np.int32) if hasattr(q, "cpu") else np.asarray(q, np.int32)
+    s = s.cpu().numpy() if hasattr(s, "cpu") else np.asarray(s, np.float32)
+    q_ref, s_ref = np.asarray(q_ref, np.int32), np.asarray(s_ref, np.float32)
+    assert np.all(np.abs(s - s_ref) <= s_ref * 2 ** -8)
+    d = np.abs(q - q_ref)
+    assert d.max(initial=0) <= 1
+    assert (d == 0).mean() >= code_frac, (d == 0).mean()
+
+
+@pytest.mark.parametrize("act", ["gelu", "gelu_tanh"])
+@pytest.mark.parametrize("M,K,group,dtype", [
+    (512, 12288, 256, torch.bfloat16),    # FLUX MLP middle (text rows)
+    (300, 3072, 256, torch.float16),
+    (129, 2048, 0, torch.bfloat16),
+    (64, 8192, 256, torch.float16),
+])
+def test_gelu_quantize_matches_unfused(gpu, act, M, K, group, dtype):
+    g = torch.Generator().manual_seed(M + K)
+    h = (torch.randn(M, K, generator=g) * 2).to(dtype).to(gpu)
+    q, s = _int8.act_quantize(h, group, act)
+    # the reference's unfused form: GELU on the GPU in float32, rounded to the dtype, then quantized
+    q_u, s_u = _int8.quantize_activation(F.gelu(h.float(), approximate=APPROX[act]).to(dtype), group)
+    _agree(q, s, q_u.cpu().numpy(), s_u.cpu().numpy())
+    # and the oracle's restatement (float64 erf / tanh rounded once to float32)
+    q_o, s_o = OQ.act_quantize(np32(h), group, APPROX[act], DT[dtype])
+    _agree(q, s, q_o, s_o)
+
+
+@pytest.mark.parametrize("M,K1,K2,dtype", [(4608, 3072, 12288, torch.bfloat16), (77, 256, 512, torch.float16)])
+def test_concat_prefix_and_gelu_tanh(gpu, M, K1, K2, dtype):
+    """FLUX single block: linear2's input is cat(attention, gelu_tanh(mlp)),
+    the mlp half a column slice of linear1's output (row stride > width)."""
+    g = torch.Generator().manual_seed(K1 + K2)
+    attn = torch.randn(M, K1, generator=g).to(dtype).to(gpu)
+    lin1 = (torch.randn(M, 3 * K1 + K2, generator=g) * 2).to(dtype).to(gpu)
+    mlp = lin1[:, 3 * K1:]
+    q, s = _int8.act_quantize(mlp, 256, "gelu_tanh", prefix=attn)
+    cat = torch.cat((attn, F.gelu(mlp.float(), approximate="tanh").to(dtype)), 1)
+    q_u, s_u = _int8.quantize_activation(cat, 256)
+    _agree(q, s, q_u.cpu().numpy(), s_u.cpu().numpy())
+    # act "none" with a prefix is an exact concatenation
+    q0, s0 = _int8.act_quantize(mlp, 256, "none", prefix=attn)
+    q0_u, s0_u = _int8.quantize_activation(torch.cat((attn, mlp), 1), 256)
+    assert torch.equal(q0, q0_u) and torch.equal(s0, s0_u)
+
+
+def test_act_quantize_rejects_unaligned_widths(gpu):
+    h = torch.randn(4, 300, device=gpu, dtype=torch.bfloat16)
+    assert not _int8.act_fusable(h)
+    with pytest.raises(RuntimeError, match="multiples of 256"):
+        _int8.act_quantize(h, 0, "gelu")
+    # gelu_quantize falls back to the unfused ops for such rows
+    q, s = _int8.gelu_quantize(h, 0)
+    q_u, s_u = _int8.quantize_activation(F.gelu(h.float()).to(h.dtype), 0)
+    assert torch.equal(q, q_u) and torch.equal(s, s_u)
+
+
+@pytest.mark.parametrize("approximate,bias", [("none", False), ("tanh", True)])
+def test_int8_mlp_matches_eager(gpu, approximate, bias):
+    """int8_mlp (fused middle) against the same two Int8Linear layers run
+    eagerly, l2(gelu(l1(x))), and against the float MLP."""
+    torch.manual_seed(5)
+    d, m = 1024, 4096
+    fc1, fc2 = nn.Linear(d, m, bias=bias).to(gpu).bfloat16(), nn.Linear(m, d, bias=bias).to(gpu).bfloat16()
+    l1, l2 = _int8.Int8Linear.from_linear(fc1, 256), _int8.Int8Linear.from_linear(fc2, 256)
+    x = torch.randn(2, 333, d, device=gpu, dtype=torch.bfloat16)
+    y = _int8.int8_mlp(x, l1, l2, approximate)
+    y_eager = l2(F.gelu(l1(x), approximate=approximate))
+    assert y.shape == y_eager.shape and y.dtype == torch.bfloat16
+    assert rel_l2(np32(y), np32(y_eager)) < 2e-3
+    y_float = fc2(F.gelu(fc1(x).float(), approximate=approximate).bfloat16())
+    assert rel_l2(np32(y), np32(y_float)) < 3e-2 and cosine(np32(y), np32(y_float)) > 0.999

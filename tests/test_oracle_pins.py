@@ -298,3 +298,48 @@ def test_int8_attention_is_shift_invariant_in_keys(shift):
     base = OA.int8_attention(q, k, v, None, "bf16", "f32")
     shifted = OA.int8_attention(q, (k + np.float32(shift)).astype(np.float32), v, None, "bf16", "f32")
     np.testing.assert_allclose(shifted, base, atol=3e-2)
+
+
+# ---------------------------------------------------------------- GELU (fused MLP middle)
+
+def test_gelu_oracle_closed_forms():
+    """The erf form is x * Phi(x): Phi(1) = 0.8413447460685429, Phi(-1) =
+    0.15865525393145707, 0 at 0, x for large x, 0 for very negative x."""
+    from math import erf, sqrt
+    x = np.array([0.0, 1.0, -1.0, 2.0, 8.0, -8.0, -30.0], np.float32)
+    y = OQ.gelu(x, "none", "f16")
+    exact = np.array([v * 0.5 * (1 + erf(v / sqrt(2))) for v in x.astype(np.float64)])
+    assert np.array_equal(y, exact.astype(np.float16).astype(np.float32))
+    assert y[0] == 0 and y[4] == 8 and y[6] == 0
+
+
+def test_gelu_oracle_agrees_with_torch_after_rounding():
+    """float32 torch GELU (CPU) rounded to bf16 / fp16 equals the oracle's
+    except next to a rounding boundary. For x below about -3 both forms
+    compute 1 + erf (or 1 + tanh) next to cancellation, so a one-ulp
+    difference in the library function moves the (tiny) result by up to
+    |x| 2^-24: those elements agree to 1e-5 absolute, far below any row's
+    quantization step. The tanh form stays within 3e-3 of the erf form (its
+    known approximation error)."""
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(1 << 18, generator=g) * 3).numpy()
+    for approx in ("none", "tanh"):
+        ref = torch.nn.functional.gelu(torch.from_numpy(x), approximate=approx)
+        for dt, tdt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+            o = OQ.gelu(x, approx, dt)
+            r = ref.to(tdt).float().numpy()
+            big = np.abs(r) >= 1e-2
+            assert (o[big] == r[big]).mean() > 0.999, (approx, dt, (o[big] == r[big]).mean())
+            assert np.all(np.abs(o - r) <= np.maximum(np.abs(r) * 2 ** -7, 1e-5)), (approx, dt)
+    a, b = OQ.gelu(x, "tanh", "f16"), OQ.gelu(x, "none", "f16")
+    assert np.all(np.abs(a - b) <= 3e-3 + np.abs(b) * 2 ** -10)   # plus one fp16 ulp of rounding
+
+
+def test_act_quantize_oracle_is_quantize_of_gelu():
+    """The fused form equals quantize_activation(cat(prefix, gelu(x)))."""
+    g = np.random.default_rng(4)
+    x = g.standard_normal((5, 512)).astype(np.float32)
+    pre = g.standard_normal((5, 256)).astype(np.float32)
+    q, s = OQ.act_quantize(x, 256, "tanh", "bf16", prefix=pre)
+    q2, s2 = OQ.quantize_activation(np.concatenate([pre, OQ.gelu(x, "tanh", "bf16")], 1), 256)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
