@@ -340,6 +340,46 @@ def shapes_report(dev):
                           "quant_pct_hbm": round(100 * qbytes / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
                           "vs_int_mm_rescale": _cmp(y, ref), "vs_float_linear": _cmp(y, yf)}), flush=True)
         del x, lin, m, qx, sx, y, acc, ref, yf
+    # UNet self-attention q/k/v: separate layers, one shared quantization (the
+    # reference's Anima pattern), and one GEMM over stacked weights
+    from diffucore_amd import fuse_linears, shared_qkv
+    for name, M, K in (("sdxl_qkv_4096", 8192, 640), ("sdxl_qkv_1024", 2048, 1280)):
+        g.manual_seed(0)
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.float16)
+        projs = []
+        for _ in range(3):
+            lin = torch.nn.Linear(K, K, bias=False, device=dev)
+            with torch.no_grad():
+                lin.weight.normal_(0, 0.02, generator=g)
+            projs.append(Int8Linear.from_linear(lin, 256 if K % 256 == 0 else 0))
+        fused = fuse_linears(projs)
+        ms_sep = per_call_ms(lambda: [p(x) for p in projs])
+        ms_shared = per_call_ms(lambda: shared_qkv(x, projs))
+        ms_fused = per_call_ms(lambda: fused(x).split(K, -1))
+        exact = all(torch.equal(a, b) for a, b in zip(fused(x).split(K, -1), shared_qkv(x, projs)))
+        print(json.dumps({"kind": "qkv_projection", "shape": name, "M": M, "K": K, "N": 3 * K, "dtype": "float16",
+                          "separate_ms": round(ms_sep, 4), "shared_quant_ms": round(ms_shared, 4),
+                          "fused_gemm_ms": round(ms_fused, 4), "fused_equals_shared": exact}), flush=True)
+        del x, projs, fused
+    # fused MLP middle (dc_act_quantize_rows) against the ops it replaces, at FLUX shapes
+    from diffucore_amd import act_quantize
+    for name, M, K1, K2 in (("flux_img_mlp_middle", 4096, 0, 12288), ("flux_single_linear2_input", 4608, 3072, 12288)):
+        g.manual_seed(0)
+        h = (torch.randn(M, K2, generator=g, device=dev) * 2).to(torch.bfloat16)
+        pre = torch.randn(M, K1, generator=g, device=dev).to(torch.bfloat16) if K1 else None
+
+        def unfused():
+            a = F.gelu(h, approximate="tanh")
+            return quantize_activation(torch.cat((pre, a), 1) if K1 else a, 256)
+
+        ms_u = per_call_ms(unfused)
+        ms_f = per_call_ms(lambda: act_quantize(h, 256, "gelu_tanh", prefix=pre))
+        nbytes = M * (K1 + K2) * 2 + M * (K1 + K2) + 4 * M   # read the 16-bit rows once, write codes + scales
+        print(json.dumps({"kind": "fused_mlp_middle", "shape": name, "M": M, "K1": K1, "K2": K2, "dtype": "bfloat16",
+                          "act": "gelu_tanh", "unfused_ms": round(ms_u, 4), "fused_ms": round(ms_f, 4),
+                          "speedup": round(ms_u / ms_f, 2), "fused_GBps": round(nbytes / (ms_f * 1e-3) / 1e9, 1)}),
+              flush=True)
+        del h, pre
 
 
 # ---------------------------------------------------------------- main

@@ -316,17 +316,38 @@ __global__ void __launch_bounds__(1024) quant_rows_lds_kernel(const void* __rest
 // it (src/diffucore/models/_int8.py:433-435: 0.5 h (1 + erf(h / sqrt 2)),
 // cast to the activation dtype; the tanh form is torch's
 // gelu(approximate="tanh"), 0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))),
-// which FLUX's MLPs use).
+// which FLUX's MLPs use). Both are evaluated in forms without cancellation
+// in the negative tail and with the hardware exp2 / reciprocal (this pass is
+// VALU-bound, and the library erf / tanh cost about twice as much):
+//   tanh form: 0.5 x (1 + tanh u) = x / (1 + 2^(-2 u log2 e));
+//   erf form: 1 + erf(x / sqrt 2) = erfc(z) for x < 0, 2 - erfc(z) for x >= 0,
+//   z = |x| / sqrt 2, with erfc(z) = (a1 t + ... + a5 t^5) e^(-z^2),
+//   t = 1 / (1 + p z) (Abramowitz & Stegun 7.1.26, Hastings' approximation,
+//   |erf error| <= 1.5e-7).
+// Against float32 library GELU both stay within a few float32 ulp (absolute
+// ~1e-7 |x|), which the rounding to 16 bits hides but next to a boundary.
+constexpr float LOG2E = 1.4426950408889634f;
+
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  const float x3 = (x * x) * x;
+  const float u = 0.7978845608028654f * __builtin_fmaf(0.044715f, x3, x);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * (-2.0f * LOG2E)));
+}
+
+__device__ __forceinline__ float gelu_erf_f32(float x) {
+  const float z = fabsf(x) * 0.7071067811865476f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
+  float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  poly = __builtin_fmaf(poly, t, 1.421413741f);
+  poly = __builtin_fmaf(poly, t, -0.284496736f);
+  poly = __builtin_fmaf(poly, t, 0.254829592f);
+  const float erfc = (poly * t) * __builtin_amdgcn_exp2f((z * z) * -LOG2E);
+  return (0.5f * x) * (x < 0.0f ? erfc : 2.0f - erfc);
+}
+
 template <int DT>
 __device__ __forceinline__ float act_round(float x, int act) {
-  float y;
-  if (act == DC_ACT_GELU_ERF) {
-    y = (0.5f * x) * (1.0f + erff(x * 0.7071067811865476f));
-  } else {
-    const float inner = 0.7978845608028654f * (x + 0.044715f * ((x * x) * x));
-    y = (0.5f * x) * (1.0f + tanhf(inner));
-  }
-  return round_to<DT>(y);
+  return round_to<DT>(act == DC_ACT_GELU_ERF ? gelu_erf_f32(x) : gelu_tanh_f32(x));
 }
 
 // Rows of concat(x1, act(x2)): columns 0 .. K1 - 1 from x1 as they are,

@@ -113,3 +113,35 @@ def test_every_tile_configuration(gpu, mnk, plan):
         assert np.array_equal(np32(out).view(np.uint32), ref.view(np.uint32)), dtype
     acc = _int8.int_mm(q.to(gpu), w.to(gpu))
     assert np.array_equal(acc.cpu().numpy(), acc_ref)
+
+
+def _int8_layers(gpu, k, ns, bias, seed):
+    torch.manual_seed(seed)
+    group = 256 if k % 256 == 0 else 0
+    return [_int8.Int8Linear.from_linear(nn.Linear(k, n, bias=bias).to(gpu).half(), group) for n in ns]
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_shared_qkv_equals_separate_layers(gpu, bias):
+    """Self-attention q/k/v on one rotated + quantized copy of x (the Anima
+    pattern, anima_dit.py:307-315) equals each layer on its own (the
+    quantization is deterministic); cross-attention keeps k/v on the context."""
+    projs = _int8_layers(gpu, 640, (640, 640, 640), bias, 21)
+    x = torch.randn(2, 1000, 640, device=gpu, dtype=torch.float16)
+    got = _int8.shared_qkv(x, projs)
+    for p, y in zip(projs, got):
+        assert torch.equal(y, p(x))
+    ctx = torch.randn(2, 77, 640, device=gpu, dtype=torch.float16)
+    q, k, v = _int8.shared_qkv(x, projs, ctx, is_selfattn=False)
+    assert torch.equal(q, projs[0](x)) and torch.equal(k, projs[1](ctx)) and torch.equal(v, projs[2](ctx))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_fused_linears_equal_concatenated_outputs(gpu, bias):
+    """One GEMM over stacked weights / scales / biases gives each layer's
+    output bit for bit (per-channel scales, per-channel bias rounding)."""
+    layers = _int8_layers(gpu, 1280, (1280, 640, 2560), bias, 22)
+    fused = _int8.fuse_linears(layers)
+    x = torch.randn(3, 333, 1280, device=gpu, dtype=torch.float16)
+    y = fused(x)
+    assert torch.equal(y, torch.cat([l(x) for l in layers], -1))
