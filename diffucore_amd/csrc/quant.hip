@@ -402,6 +402,117 @@ __global__ void __launch_bounds__(1024) quant_act_rows_kernel(const void* __rest
   if (li == 0) scale[row] = sc;
 }
 
+// ---------------------------------------------------------------- LayerNorm-modulate + quantize
+
+// sum over the SEG lanes of an aligned segment (xor butterfly: every lane of
+// the segment ends with the same bits)
+template <int SEG>
+__device__ __forceinline__ float seg_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += swz_xor4(v);
+  if constexpr (SEG >= 16) v += __shfl_xor(v, 8);
+  if constexpr (SEG >= 32) v += __shfl_xor(v, 16);
+  if constexpr (SEG >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+// 8 16-bit values of MDT at p (16-byte aligned) as float32
+template <int MDT>
+__device__ __forceinline__ void load8_h16(const uint16_t* p, float (&f)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = h16_to_f32<MDT>(w[i] & 0xffffu);
+    f[2 * i + 1] = h16_to_f32<MDT>(w[i] >> 16);
+  }
+}
+
+// Rows of round_MDT(LayerNorm(x) * sc1 + sh), rotated and quantized like
+// quant_rows_lds_kernel. LayerNorm in float32 over the row: mean = sum / K,
+// then rstd = 1 / sqrt(sum((x - mean)^2) / K + eps) (two passes, no affine
+// weights), y = ((x - mean) * rstd) * sc1 + sh with separate roundings, as the
+// reference's _ln_mod_kernel (src/diffucore/models/_fused.py:73-85), whose
+// output it rounds to the 16-bit type of sc1 / sh before the quantizer reads
+// it. sc1 (the caller's 1 + scale) and sh are row row / rows_per_mod of
+// [*, K] arrays, row stride ldm. Each row sum is the segment sums (xor
+// butterflies) added in segment order.
+template <int DT, int MDT, int S, bool ROT>
+__global__ void __launch_bounds__(1024) quant_lnmod_rows_kernel(const void* __restrict__ x, int64_t ldx, int K,
+                                                                int64_t M, const uint16_t* __restrict__ sc1,
+                                                                const uint16_t* __restrict__ sh, int64_t ldm,
+                                                                int rows_per_mod, float eps, int rpb, float inv_lr,
+                                                                int8_t* __restrict__ q, int64_t ldq,
+                                                                float* __restrict__ scale) {
+  __shared__ float red[3][128];
+  const int t = threadIdx.x, r = t & 7;
+  const int G = K >> 8, lr = 8 * G;
+  const int rloc = (int)(((float)t + 0.5f) * inv_lr), li = t - rloc * lr;
+  const int64_t row = (int64_t)blockIdx.x * rpb + rloc;
+  const bool live = rloc < rpb && row < M;
+  const int q8 = ((r & 3) << 1) | (r >> 2);
+  float v[1][4][8];
+  bool ok[1][4];
+  int off[1][4];
+  load_groups<DT, 1>(x, (live ? row : 0) * ldx, K, li >> 3, live ? G : 0, q8, v, ok, off);
+  // the modulation vectors for the same elements, loaded with the row
+  float c[4][8], b[4][8];
+  const int64_t mrow = (live ? row : 0) / rows_per_mod;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = ok[0][j] ? off[0][j] : 0;
+    load8_h16<MDT>(sc1 + mrow * ldm + e, c[j]);
+    load8_h16<MDT>(sh + mrow * ldm + e, b[j]);
+  }
+  const int nseg = lr / S, s0 = (live ? rloc : 0) * nseg;
+  // mean
+  float a = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a += v[0][j][e];
+  a = seg_sum<S>(a);
+  if ((t & (S - 1)) == 0) red[0][t / S] = a;
+  __syncthreads();
+  float sum = red[0][s0];
+  for (int i = 1; i < nseg; ++i) sum += red[0][s0 + i];
+  const float mean = sum / (float)K;
+  // centered variance (elements past the row or of idle lanes contribute 0)
+  float c2 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = ok[0][j] ? v[0][j][e] - mean : 0.0f;
+      c2 += d * d;
+    }
+  c2 = seg_sum<S>(c2);
+  if ((t & (S - 1)) == 0) red[1][t / S] = c2;
+  __syncthreads();
+  float var = red[1][s0];
+  for (int i = 1; i < nseg; ++i) var += red[1][s0 + i];
+  const float rstd = 1.0f / sqrtf(var / (float)K + eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = round_to<MDT>(materialize(materialize((v[0][j][e] - mean) * rstd) * c[j][e]) + b[j][e]);
+      v[0][j][e] = ok[0][j] ? y : 0.0f;
+    }
+  if constexpr (ROT) hadamard256(v[0]);
+  const float seg = seg_max<S>(lane_amax(v));
+  if ((t & (S - 1)) == 0) red[2][t / S] = seg;
+  __syncthreads();
+  if (!live) return;
+  float amax = red[2][s0];
+  for (int i = 1; i < nseg; ++i) amax = fmaxf(amax, red[2][s0 + i]);
+  constexpr int PRE = ROT ? 16 : 1;
+  const float sc = row_scale<PRE>(amax);
+  quantize_store<1, PRE>(v, ok, off, sc, q + row * ldq);
+  if (li == 0) scale[row] = sc;
+}
+
 // Generic path (group 0, any K, any alignment): two passes over the row.
 template <int DT>
 __device__ __forceinline__ float load1(const void* base, int64_t i) {
@@ -532,6 +643,38 @@ static int launch_act(const void* x1, int64_t ld1, int K1, const void* x2, int64
   }
 }
 
+template <int DT, int MDT, bool ROT>
+static int launch_lnmod(const void* x, int64_t ldx, int K, int64_t M, const void* sc1, const void* sh, int64_t ldm,
+                        int rows_per_mod, float eps, int8_t* q, int64_t ldq, float* scale, hipStream_t st) {
+  const int G = K / 256, lr = 8 * G;
+  const int S = G % 8 == 0 ? 64 : G % 4 == 0 ? 32 : G % 2 == 0 ? 16 : 8;
+  int rpb = 8 / (S / 8);
+  while (rpb > 1 && rpb * lr > 1024) rpb /= 2;
+  const int nt = (rpb * lr + 63) / 64 * 64;
+  const dim3 grid((unsigned)((M + rpb - 1) / rpb));
+  const auto* c = static_cast<const uint16_t*>(sc1);
+  const auto* b = static_cast<const uint16_t*>(sh);
+  const float il = 1.0f / (float)lr;
+  switch (S) {
+    case 64: hipLaunchKernelGGL((quant_lnmod_rows_kernel<DT, MDT, 64, ROT>), grid, dim3(nt), 0, st, x, ldx, K, M, c, b, ldm, rows_per_mod, eps, rpb, il, q, ldq, scale); break;
+    case 32: hipLaunchKernelGGL((quant_lnmod_rows_kernel<DT, MDT, 32, ROT>), grid, dim3(nt), 0, st, x, ldx, K, M, c, b, ldm, rows_per_mod, eps, rpb, il, q, ldq, scale); break;
+    case 16: hipLaunchKernelGGL((quant_lnmod_rows_kernel<DT, MDT, 16, ROT>), grid, dim3(nt), 0, st, x, ldx, K, M, c, b, ldm, rows_per_mod, eps, rpb, il, q, ldq, scale); break;
+    default: hipLaunchKernelGGL((quant_lnmod_rows_kernel<DT, MDT, 8, ROT>), grid, dim3(nt), 0, st, x, ldx, K, M, c, b, ldm, rows_per_mod, eps, rpb, il, q, ldq, scale); break;
+  }
+  return launch_status("quant_lnmod_rows_kernel");
+}
+
+template <int MDT>
+static int dispatch_lnmod(const void* x, int x_dtype, int64_t ldx, int K, int64_t M, const void* sc1, const void* sh,
+                          int64_t ldm, int rows_per_mod, float eps, int group, int8_t* q, int64_t ldq, float* scale,
+                          hipStream_t st) {
+  if (x_dtype == DC_F32)
+    return group ? launch_lnmod<DC_F32, MDT, true>(x, ldx, K, M, sc1, sh, ldm, rows_per_mod, eps, q, ldq, scale, st)
+                 : launch_lnmod<DC_F32, MDT, false>(x, ldx, K, M, sc1, sh, ldm, rows_per_mod, eps, q, ldq, scale, st);
+  return group ? launch_lnmod<MDT, MDT, true>(x, ldx, K, M, sc1, sh, ldm, rows_per_mod, eps, q, ldq, scale, st)
+               : launch_lnmod<MDT, MDT, false>(x, ldx, K, M, sc1, sh, ldm, rows_per_mod, eps, q, ldq, scale, st);
+}
+
 }  // namespace dc
 
 using namespace dc;
@@ -583,4 +726,31 @@ extern "C" int dc_act_quantize_rows(const void* x1, int64_t ld1, int64_t K1, con
                  : launch_act<DC_BF16, false>(a, la, (int)K1, b, lb, (int)K, act, M, q, ldq, scale, st);
   return group ? launch_act<DC_F16, true>(a, la, (int)K1, b, lb, (int)K, act, M, q, ldq, scale, st)
                : launch_act<DC_F16, false>(a, la, (int)K1, b, lb, (int)K, act, M, q, ldq, scale, st);
+}
+
+extern "C" int dc_ln_mod_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* sc1,
+                                       const void* shift, int mod_dtype, int64_t ldm, int64_t rows_per_mod, float eps,
+                                       int group, int8_t* q, int64_t ldq, float* scale, void* stream) {
+  clear_error();
+  if (M < 0 || K <= 0 || ldx < K || ldq < K || ldm < K || rows_per_mod <= 0 || rows_per_mod > 0x7fffffff)
+    return fail(DC_EINVAL, "dc_ln_mod_quantize_rows: bad M/K/ldx/ldq/ldm/rows_per_mod");
+  if (M == 0) return DC_OK;
+  if (M > 0x7fffffff) return fail(DC_EINVAL, "dc_ln_mod_quantize_rows: M too large");
+  if (!x || !sc1 || !shift || !q || !scale) return fail(DC_EINVAL, "dc_ln_mod_quantize_rows: null pointer");
+  if (group != 0 && group != 256) return fail(DC_EINVAL, "dc_ln_mod_quantize_rows: group must be 0 or 256");
+  if (mod_dtype != DC_F16 && mod_dtype != DC_BF16)
+    return fail(DC_EINVAL, "dc_ln_mod_quantize_rows: mod_dtype must be DC_F16 or DC_BF16");
+  if (x_dtype != mod_dtype && x_dtype != DC_F32)
+    return fail(DC_EINVAL, "dc_ln_mod_quantize_rows: x_dtype must be mod_dtype or DC_F32");
+  if (!(eps >= 0.0f)) return fail(DC_EINVAL, "dc_ln_mod_quantize_rows: eps must be >= 0");
+  const int eb = elem_bytes(x_dtype);
+  if (K % 256 || K > 32768 || !aligned16(x) || (ldx * eb) % 16 || !aligned16(sc1) || !aligned16(shift) || ldm % 8 ||
+      (reinterpret_cast<uintptr_t>(q) & 7) || ldq % 8)
+    return fail(DC_EUNSUPPORTED, "dc_ln_mod_quantize_rows: needs K a multiple of 256 (<= 32768) and 16-byte aligned rows");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (mod_dtype == DC_BF16)
+    return dispatch_lnmod<DC_BF16>(x, x_dtype, ldx, (int)K, M, sc1, shift, ldm, (int)rows_per_mod, eps, group, q, ldq,
+                                   scale, st);
+  return dispatch_lnmod<DC_F16>(x, x_dtype, ldx, (int)K, M, sc1, shift, ldm, (int)rows_per_mod, eps, group, q, ldq,
+                                scale, st);
 }

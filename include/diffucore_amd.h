@@ -74,6 +74,26 @@ int dc_act_quantize_rows(const void* x1, int64_t ld1, int64_t K1, const void* x2
                          void* stream);
 
 /*
+ * dc_quantize_rows of the rows of y = round(LayerNorm(x) * sc1 + shift), in one
+ * pass: LayerNorm without affine weights in float32 (mean, then the centered
+ * variance, rstd = 1 / sqrt(var + eps)), y in float32 with separate roundings,
+ * rounded to mod_dtype (DC_F16 or DC_BF16) before the rotation and the codes.
+ *   x [M, K] of x_dtype (mod_dtype or DC_F32), row stride ldx;
+ *   sc1 (the caller's 1 + scale) and shift: row m / rows_per_mod of [*, K]
+ *   arrays of mod_dtype, row stride ldm (rows_per_mod rows share one row, e.g.
+ *   the tokens of one sample);
+ *   q [M, K] int8 (row stride ldq), scale [M] as dc_quantize_rows.
+ * K % 256 == 0, K <= 32768, 16-byte aligned rows.
+ * Replaces the reference's LayerNorm-modulate glue (src/diffucore/models/
+ * _fused.py:73-85 _ln_mod_kernel, ln_mod :151-156; eager in flux_dit.py's
+ * blocks) followed by quantize_activation in the next Int8Linear: the
+ * modulated rows are never written out.
+ */
+int dc_ln_mod_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const void* sc1,
+                            const void* shift, int mod_dtype, int64_t ldm, int64_t rows_per_mod, float eps,
+                            int group, int8_t* q, int64_t ldq, float* scale, void* stream);
+
+/*
  * W8A8 GEMM on int8 MFMA with int32 accumulation and a fused epilogue.
  *   a   [M, K] int8 (activations), row stride lda
  *   w   [N, K] int8 (nn.Linear weight layout), row stride ldw

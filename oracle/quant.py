@@ -10,6 +10,8 @@ Follows reference ``src/diffucore/models/_int8.py``:
 * ``rotate_matmul``  <- ``_rotate`` (``_int8.py:79-84``): ``t @ H`` per group.
 * ``rotate_butterfly`` <- ``_hadamard_rows`` (``_int8.py:363-372``), with the
   summation order this build fixes (see its docstring).
+* ``ln_mod_quantize`` <- the LayerNorm-modulate glue ``_ln_mod_kernel``
+  (``_fused.py:73-85``) followed by ``quantize_activation``.
 * ``gelu`` / ``act_quantize`` <- the fused MLP middle ``_gelu`` and
   ``_gelu_f16_rot_quant_kernel`` (``_int8.py:433-443``, ``_gelu_quantize``
   ``:348-358``); the tanh form is torch's ``gelu(approximate="tanh")`` that
@@ -136,3 +138,23 @@ def act_quantize(x2, group: int, approximate: str = "none", dtype: str = "bf16",
     if prefix is not None:
         h = np.concatenate([np.asarray(prefix, np.float32), h], axis=-1)
     return quantize_activation(h, group)
+
+
+def ln_mod_quantize(x, sc1, shift, rows_per_mod: int, eps: float, group: int, dtype: str = "bf16"):
+    """``quantize_activation`` of ``round(LayerNorm(x) * sc1 + shift)``: the
+    reference's ``_ln_mod_kernel`` (``_fused.py:73-85``) in float32 - mean =
+    sum / K, centered variance, rstd = 1 / sqrt(var + eps), y = ((x - mean) *
+    rstd) * sc1 + shift with separate roundings - rounded to ``dtype``. The
+    row sums are float32 in numpy's order; the kernel's order differs, so
+    parity is within the last bits of the mean and rstd."""
+    x = np.asarray(x, np.float32)
+    sc1 = np.asarray(sc1, np.float32)
+    shift = np.asarray(shift, np.float32)
+    K = x.shape[1]
+    m = np.arange(x.shape[0]) // rows_per_mod
+    mean = (x.sum(axis=1, dtype=np.float32) / np.float32(K)).astype(np.float32)
+    xc = (x - mean[:, None]).astype(np.float32)
+    var = ((xc * xc).sum(axis=1, dtype=np.float32) / np.float32(K)).astype(np.float32)
+    rstd = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    y = (((xc * rstd[:, None]).astype(np.float32) * sc1[m]).astype(np.float32) + shift[m]).astype(np.float32)
+    return quantize_activation(round_to(y, dtype), group)

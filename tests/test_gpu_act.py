@@ -102,3 +102,49 @@ def test_int8_mlp_matches_eager(gpu, approximate, bias):
     assert rel_l2(np32(y), np32(y_eager)) < 2e-3
     y_float = fc2(F.gelu(fc1(x).float(), approximate=approximate).bfloat16())
     assert rel_l2(np32(y), np32(y_float)) < 3e-2 and cosine(np32(y), np32(y_float)) > 0.999
+
+
+@pytest.mark.parametrize("M,K,rpm,group,xdt,mdt", [
+    (4096, 3072, 4096, 256, torch.bfloat16, torch.bfloat16),   # FLUX image stream, one sample
+    (2 * 512, 3072, 512, 256, torch.bfloat16, torch.bfloat16), # two samples of text rows
+    (333, 2048, 111, 0, torch.float32, torch.float16),          # fp32 residual stream (reference ln_mod)
+])
+def test_ln_mod_quantize_matches_unfused(gpu, M, K, rpm, group, xdt, mdt):
+    """One pass of LayerNorm-modulate + quantize against the reference's
+    ln_mod formulation computed with torch float32 ops on the GPU, rounded to
+    the modulation dtype and then quantized (and against the oracle): the row
+    statistics are sums in different orders, so parity is within the last
+    bits (the _agree bound)."""
+    g = torch.Generator().manual_seed(M + K)
+    x = (torch.randn(M, K, generator=g) * 3 + 0.5).to(xdt).to(gpu)
+    n = M // rpm
+    sc1 = (1 + torch.randn(n, K, generator=g) * 0.1).to(mdt).to(gpu)
+    sh = (torch.randn(n, K, generator=g) * 0.1).to(mdt).to(gpu)
+    q, s = _int8.ln_mod_quantize(x, sc1, sh, rpm, 1e-6, group)
+    xf = x.float()
+    mean = xf.mean(1, keepdim=True)
+    xc = xf - mean
+    y = xc * torch.rsqrt((xc * xc).mean(1, keepdim=True) + 1e-6)
+    idx = torch.arange(M, device=gpu) // rpm
+    y = (y * sc1.float()[idx] + sh.float()[idx]).to(mdt)
+    q_u, s_u = _int8.quantize_activation(y, group)
+    _agree(q, s, q_u.cpu().numpy(), s_u.cpu().numpy())
+    q_o, s_o = OQ.ln_mod_quantize(np32(x), np32(sc1), np32(sh), rpm, 1e-6, group, DT[mdt])
+    _agree(q, s, q_o, s_o)
+
+
+def test_ln_mod_quantize_strided_modulation(gpu):
+    """Modulation rows as FLUX's Modulation produces them: chunks of one
+    [B, 6K] projection (row stride 6K)."""
+    B, L, K = 2, 256, 3072
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(B * L, K, generator=g).to(torch.bfloat16).to(gpu)
+    mod = (torch.randn(B, 6 * K, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    shift, scale = mod[:, :K], mod[:, K:2 * K]
+    sc1 = (1 + scale).contiguous()
+    q, s = _int8.ln_mod_quantize(x, sc1, shift.contiguous(), L, 1e-6, 256)
+    # the strided shift view gives the same result as its contiguous copy
+    sc1_s = torch.empty(B, 6 * K, device=gpu, dtype=torch.bfloat16)[:, :K]
+    sc1_s.copy_(sc1)
+    q2, s2 = _int8.ln_mod_quantize(x, sc1_s, shift, L, 1e-6, 256)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
