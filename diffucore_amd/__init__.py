@@ -4,14 +4,16 @@ with the reference's Python operator surface on top."""
 
 from ._attention import (attention_bhld, attention_blhd, fa2_turing_available, int8_attention,
                          int8_turing_available, resolve_attention_backend, set_attention_backend)
-from ._int8 import (GROUP, Int8Linear, act_quantize, dequantize_linears, dequantize_weight, fuse_linears,
-                    gelu_quantize, int8_fast_available, int8_mlp, int_mm, ln_mod_quantize, quantize_activation,
+from ._int8 import (GROUP, Int8Embedding, Int8Linear, act_quantize, adopt_int8_embedding, adopt_int8_layers,
+                    dequantize_linears, dequantize_weight, fuse_linears, gelu_quantize, int8_fast_available,
+                    int8_layers, int8_mlp, int_mm, ln_mod_quantize, lora_seed, quantize_activation,
                     quantize_linears, quantize_weight, rescale, scaled_mm, shared_qkv)
 from .runtime import DevicePolicy
 
 __all__ = [
     "GROUP", "DevicePolicy", "Int8Linear", "act_quantize", "attention_bhld", "attention_blhd", "dequantize_linears",
-    "fuse_linears", "ln_mod_quantize", "shared_qkv",
+    "fuse_linears", "ln_mod_quantize", "shared_qkv", "Int8Embedding", "adopt_int8_embedding", "adopt_int8_layers",
+    "int8_layers", "lora_seed",
     "dequantize_weight", "fa2_turing_available", "gelu_quantize", "int8_attention", "int8_fast_available",
     "int8_mlp",
     "int8_turing_available", "int_mm", "quantize_activation", "quantize_linears", "quantize_weight",

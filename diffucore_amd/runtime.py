@@ -9,20 +9,22 @@ from dataclasses import dataclass
 import torch
 
 
+ATTENTION_BACKENDS = ("sdpa", "auto", "fa2_turing", "int8_turing")
+
+
 @dataclass
 class DevicePolicy:
     device: torch.device
     compute_dtype: torch.dtype = torch.float16
-    # "sdpa" (default, exact), "int8_turing" (the INT8 kernels: fp16/bf16,
-    # self-attention), "fa2_turing" (never available on MI355X) or "auto".
+    # one of ATTENTION_BACKENDS: "sdpa" is exact and the default;
+    # "int8_turing" runs self-attention on the INT8 kernels (fp16 / bf16);
+    # "fa2_turing" never runs on MI355X; "auto" picks the best that can
     attention: str = "sdpa"
-    # quantize the backbone's block linears to W8A8 at load
+    # W8A8-quantize the backbone's block linears when loading
     int8: bool = False
     compile: bool = False
 
     def __post_init__(self):
-        if self.attention not in ("sdpa", "auto", "fa2_turing", "int8_turing"):
-            raise ValueError(
-                f"attention must be 'sdpa', 'auto', 'fa2_turing', or 'int8_turing'; "
-                f"got {self.attention!r}"
-            )
+        if self.attention not in ATTENTION_BACKENDS:
+            allowed = ", ".join(repr(b) for b in ATTENTION_BACKENDS)
+            raise ValueError(f"attention must be one of {allowed}; got {self.attention!r}")
