@@ -380,6 +380,46 @@ def shapes_report(dev):
                           "speedup": round(ms_u / ms_f, 2), "fused_GBps": round(nbytes / (ms_f * 1e-3) / 1e9, 1)}),
               flush=True)
         del h, pre
+    # QK RMSNorm + rotary (dc_qk_norm_rope) against FLUX's eager ops, at the FLUX double-block shape:
+    # txt (512) and img (4096) q/k/v views of the two qkv projections -> joint (B, H, L, D) q, k, v
+    import flux_step as FS
+    from diffucore_amd import flux_qk_norm_rope
+    H, D, Lt, Li = 24, 128, 512, 4096
+    g.manual_seed(0)
+    tqkv = torch.randn(1, Lt, 3 * H * D, generator=g, device=dev).to(torch.bfloat16)
+    iqkv = torch.randn(1, Li, 3 * H * D, generator=g, device=dev).to(torch.bfloat16)
+    sc = [torch.rand(D, generator=g, device=dev).add(0.5).to(torch.bfloat16) for _ in range(4)]
+    pe = FS.position_embedding(FS.FluxShape(), dev)
+    qn = [FS.RMSNorm(D).to(dev, torch.bfloat16) for _ in range(4)]
+    for n, s_ in zip(qn, sc):
+        n.scale.data.copy_(s_)
+
+    def eager():
+        iq, ik, iv = FS._split_heads(iqkv, H)
+        tq, tk, tv = FS._split_heads(tqkv, H)
+        iq, ik = qn[0](iq).to(iv), qn[1](ik).to(iv)
+        tq, tk = qn[2](tq).to(tv), qn[3](tk).to(tv)
+        q, k = FS.apply_rope(torch.cat((tq, iq), 2), torch.cat((tk, ik), 2), pe)
+        return q, k, torch.cat((tv, iv), 2)
+
+    bufs = [torch.empty(1, Lt + Li, H, D, device=dev, dtype=torch.bfloat16) for _ in range(3)]
+
+    def fused():
+        for x, a, b, sl in ((tqkv, qn[2], qn[3], slice(0, Lt)), (iqkv, qn[0], qn[1], slice(Lt, Lt + Li))):
+            x5 = x.unflatten(-1, (3, H, D))
+            flux_qk_norm_rope(x5[:, :, 0], x5[:, :, 1], a.scale, b.scale, pe[:, :, sl], v=x5[:, :, 2],
+                              out=tuple(t[:, sl] for t in bufs))
+        return bufs
+
+    ms_e, ms_f = per_call_ms(eager), per_call_ms(fused)
+    eq = eager()
+    fused()
+    same = [float((a.transpose(1, 2) == b).float().mean()) for a, b in zip(eq, bufs)]
+    nbytes = 3 * 2 * (Lt + Li) * H * D * 2    # q, k, v: 16-bit rows read once and written once
+    print(json.dumps({"kind": "qk_norm_rope", "shape": "flux_double_block", "L": Lt + Li, "H": H, "D": D,
+                      "dtype": "bfloat16", "eager_ms": round(ms_e, 4), "fused_ms": round(ms_f, 4),
+                      "speedup": round(ms_e / ms_f, 2), "fused_GBps": round(nbytes / (ms_f * 1e-3) / 1e9, 1),
+                      "bit_equal_fraction_q_k_v": [round(x, 5) for x in same]}), flush=True)
 
 
 # ---------------------------------------------------------------- main
@@ -412,7 +452,7 @@ def main():
         return
 
     import flux_step as FS
-    from diffucore_amd import _lib, quantize_linears, set_attention_backend
+    from diffucore_amd import _lib, quantize_linears, set_attention_backend, set_fused_glue
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -428,10 +468,16 @@ def main():
         with torch.no_grad():
             bf16_ms = time_steps(lambda: model(x0, txt, sigmas[:1].to(x0.dtype), y, pe), 3, 1)
             lat_bf16 = FS.denoise(model, x0, txt, y, pe, sigmas)
+        log("full step, bf16 SDPA + bf16 linears + fused QK norm/rotary glue")
+        set_fused_glue(model, True)
+        with torch.no_grad():
+            bf16_glue_ms = time_steps(lambda: model(x0, txt, sigmas[:1].to(x0.dtype), y, pe), 3, 1)
+        set_fused_glue(model, False)
     log("quantizing block linears to W8A8 (ConvRot group 256), stamping int8_turing")
     names = FS.block_linear_names(model)
     quantize_linears(model, names, dev, 256)
     set_attention_backend(model, "int8_turing")
+    set_fused_glue(model, True)
     torch.cuda.empty_cache()
     if not args.no_full:
         log("full step, INT8 attention + W8A8 linears")
@@ -441,10 +487,13 @@ def main():
         a, b = lat_int8.float().flatten(), lat_bf16.float().flatten()
         extra["denoise_step"] = {
             "int8_ms": round(int8_ms, 3), "bf16_ms": round(bf16_ms, 3), "speedup": round(bf16_ms / int8_ms, 3),
+            "bf16_fused_glue_ms": round(bf16_glue_ms, 3),
             "latent_rel_l2_vs_bf16": round(float((a - b).norm() / b.norm()), 5),
             "latent_cos_vs_bf16": round(float(a @ b / (a.norm() * b.norm())), 6),
             "what": "full synthetic FLUX.1-schnell forward + euler update at 1024^2 (flux_step.py), "
-                    "4-step final latent compared",
+                    "4-step final latent compared; int8 = W8A8 linears + INT8 attention + fused glue "
+                    "(LayerNorm-modulate/GELU quantize passes, QK norm + rotary); bf16 = the reference's "
+                    "eager ops, bf16_fused_glue = bf16 with only the QK norm + rotary pass fused",
         }
         log(f"full step: int8 {int8_ms:.2f} ms vs bf16 {bf16_ms:.2f} ms")
 

@@ -8,14 +8,15 @@ from ._int8 import (GROUP, Int8Embedding, Int8Linear, act_quantize, adopt_int8_e
                     dequantize_linears, dequantize_weight, fuse_linears, gelu_quantize, int8_fast_available,
                     int8_layers, int8_mlp, int_mm, ln_mod_quantize, lora_seed, quantize_activation,
                     quantize_linears, quantize_weight, rescale, scaled_mm, shared_qkv)
+from ._qknorm import flux_qk_norm_rope, norm_rope, qk_norm_rope, qk_ok, set_fused_glue
 from .runtime import DevicePolicy
 
-__all__ = [
-    "GROUP", "DevicePolicy", "Int8Linear", "act_quantize", "attention_bhld", "attention_blhd", "dequantize_linears",
-    "fuse_linears", "ln_mod_quantize", "shared_qkv", "Int8Embedding", "adopt_int8_embedding", "adopt_int8_layers",
-    "int8_layers", "lora_seed",
-    "dequantize_weight", "fa2_turing_available", "gelu_quantize", "int8_attention", "int8_fast_available",
-    "int8_mlp",
-    "int8_turing_available", "int_mm", "quantize_activation", "quantize_linears", "quantize_weight",
-    "rescale", "resolve_attention_backend", "scaled_mm", "set_attention_backend",
-]
+__all__ = sorted([
+    "GROUP", "DevicePolicy", "Int8Embedding", "Int8Linear", "act_quantize", "adopt_int8_embedding",
+    "adopt_int8_layers", "attention_bhld", "attention_blhd", "dequantize_linears", "dequantize_weight",
+    "fa2_turing_available", "flux_qk_norm_rope", "fuse_linears", "gelu_quantize", "int8_attention",
+    "int8_fast_available", "int8_layers", "int8_mlp", "int8_turing_available", "int_mm", "ln_mod_quantize",
+    "lora_seed", "norm_rope", "qk_norm_rope", "qk_ok", "quantize_activation", "quantize_linears",
+    "quantize_weight", "rescale", "resolve_attention_backend", "scaled_mm", "set_attention_backend",
+    "set_fused_glue", "shared_qkv",
+])

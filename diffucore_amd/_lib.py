@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libdiffucore_amd.so"
 
 F16, BF16, F32, I32, NONE = 0, 1, 2, 3, -1
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _DTYPE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int32: I32}
 
@@ -32,6 +32,10 @@ _SIGS = {
     "dc_rescale": (_I, [_P, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P]),
     "dc_ln_mod_quantize_rows": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, ctypes.c_float, _I, _P, _I64, _P, _P]),
     "dc_act_quantize_rows": (_I, [_P, _I64, _I64, _P, _I64, _I64, _I, _I, _I64, _I, _P, _I64, _P, _P]),
+    "dc_qk_norm_rope": (_I, [_I, _I64, _I64, _I64, _I64, _I, ctypes.c_float,
+                             _P, ctypes.POINTER(_I64), _P, _P, ctypes.POINTER(_I64), _P, _I,
+                             _P, _I64, _I64, _P, ctypes.POINTER(_I64), _P, ctypes.POINTER(_I64),
+                             _P, ctypes.POINTER(_I64), _P, ctypes.POINTER(_I64), _P]),
     "dc_int8_attn_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "dc_int8_attn_plan": (_I, [_I, _I, _I, _I, _I, _I] + [ctypes.POINTER(_I)] * 3),
     "dc_int8_attn_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I,

@@ -16,7 +16,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libdiffucore_amd.so"
-SOURCES = ["quant.hip", "gemm.hip", "attn.hip", "capi.cpp"]
+SOURCES = ["quant.hip", "qknorm.hip", "gemm.hip", "attn.hip", "capi.cpp"]
 ARCH = "gfx950"
 
 FLAGS = [

@@ -93,6 +93,40 @@ int dc_ln_mod_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, in
                             const void* shift, int mod_dtype, int64_t ldm, int64_t rows_per_mod, float eps,
                             int group, int8_t* q, int64_t ldq, float* scale, void* stream);
 
+/* Flags of dc_qk_norm_rope. */
+enum {
+  DC_QK_ROPE_HALF = 1,   /* rotary pairs (i, i + D/2) (Anima); otherwise (2i, 2i + 1) (FLUX) */
+  DC_QK_WEIGHT_F32 = 2   /* n = round(w * (x * rrms)) (Anima); otherwise round(round(x * rrms) * w) (FLUX) */
+};
+
+/*
+ * Per-head RMSNorm of q and k, then the rotary embedding, in one pass; also
+ * copies v when given (to gather several streams' v into one buffer).
+ *   q, k, v       [B, L, H, D] of dtype (DC_F16 or DC_BF16), element strides
+ *                 {b, l, h} in *_strides, D contiguous; k and v may be NULL;
+ *   *_out         [B, L, H, D] outputs, strides in *_out_strides (may alias
+ *                 the input with the same strides);
+ *   q/k_weight    [D] of weight_dtype (dtype or DC_F32);
+ *   rrms          rsqrt(sum(x^2) / D + eps), x^2 and the sum in float32;
+ *   freqs         float32 [.., L, D/2, 2, 2] rotary matrices, position l of
+ *                 sample b at freqs + b * freqs_batch_stride + l *
+ *                 freqs_pos_stride; NULL for no rotary embedding. A pair
+ *                 (a, b) becomes (round(f00 a + f01 b), round(f10 a + f11 b)),
+ *                 each product and sum rounded to float32 on its own.
+ * D in {32, 64, 128, 256}; 16-byte aligned rows and tables.
+ * Replaces FLUX's QKNorm + apply_rope (src/diffucore/models/flux_dit.py:
+ * 129-151, 179-184; eager torch ops) with flags 0, and Anima's
+ * qk_norm_rope (_fused.py:114-139, 174-185) with DC_QK_ROPE_HALF |
+ * DC_QK_WEIGHT_F32.
+ */
+int dc_qk_norm_rope(int dtype, int64_t B, int64_t L, int64_t H, int64_t D, int flags, float eps,
+                    const void* q, const int64_t* q_strides, const void* q_weight,
+                    const void* k, const int64_t* k_strides, const void* k_weight, int weight_dtype,
+                    const float* freqs, int64_t freqs_batch_stride, int64_t freqs_pos_stride,
+                    void* q_out, const int64_t* q_out_strides, void* k_out, const int64_t* k_out_strides,
+                    const void* v, const int64_t* v_strides, void* v_out, const int64_t* v_out_strides,
+                    void* stream);
+
 /*
  * W8A8 GEMM on int8 MFMA with int32 accumulation and a fused epilogue.
  *   a   [M, K] int8 (activations), row stride lda

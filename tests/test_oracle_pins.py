@@ -343,3 +343,107 @@ def test_act_quantize_oracle_is_quantize_of_gelu():
     q, s = OQ.act_quantize(x, 256, "tanh", "bf16", prefix=pre)
     q2, s2 = OQ.quantize_activation(np.concatenate([pre, OQ.gelu(x, "tanh", "bf16")], 1), 256)
     assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+# ---------------------------------------------------------------- QK RMSNorm + rotary (oracle/glue.py)
+
+from oracle import glue as OGL  # noqa: E402
+
+
+def _rot_table(L, half, seed=0):
+    """FLUX-style rotation matrices [[cos, -sin], [sin, cos]] per (position, pair)."""
+    ang = np.random.default_rng(seed).uniform(-np.pi, np.pi, (L, half))
+    c, s = np.cos(ang), np.sin(ang)
+    return np.stack([np.stack([c, -s], -1), np.stack([s, c], -1)], -2).astype(np.float32)
+
+
+def test_glue_identity_table_leaves_the_norm():
+    x = _f32(RNG.standard_normal((2, 5, 3, 64)))
+    w = _f32(RNG.uniform(0.5, 1.5, 64))
+    eye = np.broadcast_to(np.eye(2, dtype=np.float32), (5, 32, 2, 2))
+    for half, wf in ((False, False), (True, True)):
+        n = OGL.qk_norm(x, w, 1e-6, "bf16", wf)
+        assert np.array_equal(OGL.qk_norm_rope(x, w, eye, 1e-6, "bf16", half, wf), n)
+
+
+def test_glue_norm_against_float64():
+    """w = 1: n is the dtype rounding of x / sqrt(mean(x^2) + eps), up to one
+    float32 ulp of rrms before the rounding."""
+    x = _f32(RNG.standard_normal((4, 7, 2, 128)) * 3)
+    ones = np.ones(128, np.float32)
+    for dt, ulp in (("bf16", 2.0 ** -8), ("f16", 2.0 ** -11)):
+        n = OGL.qk_norm(x, ones, 1e-6, dt, False)
+        exact = x.astype(np.float64) / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-6)
+        assert np.all(np.abs(n - exact) <= ulp * np.abs(exact) + 1e-30)
+
+
+def test_glue_rotation_direction_and_pair_layout():
+    """(1, 0) turned by +90 degrees is (0, 1) with FLUX's matrix
+    [[cos, -sin], [sin, cos]]; a transposed matrix or a swapped pair layout
+    gives (0, -1) or moves other channels."""
+    D, L = 8, 1
+    f = _rot_table(L, D // 2)
+    f[0, 1] = [[0.0, -1.0], [1.0, 0.0]]           # pair 1 turns by +90 degrees
+    f[0, [0, 2, 3]] = np.eye(2, dtype=np.float32)
+    n = np.zeros((1, L, 1, D), np.float32)
+    n[..., 2] = 1.0                               # interleaved: pair 1 is channels (2, 3)
+    out = OGL.rope(n, f, "f32", half_pairs=False)
+    assert np.array_equal(out[0, 0, 0], [0, 0, 0, 1, 0, 0, 0, 0])
+    n = np.zeros((1, L, 1, D), np.float32)
+    n[..., 1] = 1.0                               # half split: pair 1 is channels (1, 5)
+    out = OGL.rope(n, f, "f32", half_pairs=True)
+    assert np.array_equal(out[0, 0, 0], [0, 0, 0, 0, 0, 1, 0, 0])
+    # pair lengths are kept by rotations (to rounding)
+    x = _f32(RNG.standard_normal((1, 3, 2, 16)))
+    f = _rot_table(3, 8, seed=1)
+    for half in (False, True):
+        o = OGL.rope(x, f, "f32", half)
+        pa = (lambda t: (t[..., :8], t[..., 8:])) if half else (lambda t: (t[..., 0::2], t[..., 1::2]))
+        (xa, xb), (oa, ob) = pa(x), pa(o)
+        np.testing.assert_allclose(oa ** 2 + ob ** 2, xa ** 2 + xb ** 2, rtol=1e-5)
+
+
+def _torch_flux(x, scale, pe, dtype):
+    """flux_dit.py's RMSNorm + apply_rope as torch CPU ops (the reference's
+    reshape-and-broadcast route, not the oracle's slicing)."""
+    xt = torch.from_numpy(x).to(dtype)
+    xf = xt.float()
+    rr = torch.rsqrt(torch.mean(xf ** 2, dim=-1, keepdim=True) + 1e-6)
+    n = (xf * rr).to(dtype) * torch.from_numpy(scale).to(dtype)
+    pe_t = torch.from_numpy(pe)[:, None]                       # [L, 1, D/2, 2, 2] over heads
+    n_ = n.float().reshape(*n.shape[:-1], -1, 1, 2)
+    out = pe_t[..., 0] * n_[..., 0] + pe_t[..., 1] * n_[..., 1]
+    return out.reshape(*n.shape).to(dtype).float().numpy()
+
+
+def _torch_anima(x, w, f, eps, dtype):
+    """_fused.py's Anima q/k formulas as torch CPU ops on (x[:D/2], x[D/2:])."""
+    xt = torch.from_numpy(x).to(dtype).float()
+    half = x.shape[-1] // 2
+    xa, xb = xt[..., :half], xt[..., half:]
+    r = torch.rsqrt(((xa * xa).sum(-1) + (xb * xb).sum(-1)) / x.shape[-1] + eps)[..., None]
+    wt = torch.from_numpy(w).float()
+    na = (wt[:half] * (xa * r)).to(dtype).float()
+    nb = (wt[half:] * (xb * r)).to(dtype).float()
+    ft = torch.from_numpy(f)[:, None]                          # [L, 1, D/2, 2, 2]
+    oa = (ft[..., 0, 0] * na + ft[..., 0, 1] * nb).to(dtype)
+    ob = (ft[..., 1, 0] * na + ft[..., 1, 1] * nb).to(dtype)
+    return torch.cat((oa, ob), -1).float().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_glue_against_the_reference_formulas_in_torch(dtype):
+    """The oracle against torch statements of both reference formulas: equal
+    except where the sum order or rsqrt moves rrms by a float32 ulp and a
+    rounding flips (then within one dtype ulp of the pair's size)."""
+    dt = {torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    ulp = {"bf16": 2.0 ** -7, "f16": 2.0 ** -10}[dt]
+    x = _f32(RNG.standard_normal((2, 40, 3, 128)) * 2)
+    x = OF.round_to(x, dt)
+    w = OF.round_to(_f32(RNG.uniform(0.5, 1.5, 128)), dt)
+    pe = _rot_table(40, 64, seed=2)
+    for got, want in ((OGL.qk_norm_rope(x, w, pe, 1e-6, dt), _torch_flux(x, w, pe, dtype)),
+                      (OGL.qk_norm_rope(x, w, pe, 1e-5, dt, True, True), _torch_anima(x, w, pe, 1e-5, dtype))):
+        diff = np.abs(got - want)
+        assert (diff == 0).mean() > 0.99
+        assert np.all(diff <= ulp * (np.abs(want) + 4.0))

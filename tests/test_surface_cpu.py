@@ -210,6 +210,21 @@ def test_argument_checks_fail_before_any_launch():
     assert b"head dim" in so.dc_last_error()
     assert so.dc_int8_attn_fwd(16, 16, 16, 16, _lib.F32, 1, 1, 4, 4, 64, st, st, st, st, 0.1, 16, 1 << 20,
                                None) == 1
+    # dc_qk_norm_rope: argument order (dtype, B, L, H, D, flags, eps, q, q_strides, q_weight, k, k_strides,
+    # k_weight, weight_dtype, freqs, fb, fl, q_out, qo_strides, k_out, ko_strides, v, v_strides, v_out,
+    # vo_strides, stream)
+    none = [None] * 3
+
+    def qk(dtype, B, D, flags=0, eps=1e-6, wdt=_lib.BF16):
+        return so.dc_qk_norm_rope(dtype, B, 8, 2, D, flags, eps, 16, st, 16, *none, wdt, None, 0, 0, 16, st,
+                                  None, None, None, None, None, None, None)
+
+    assert qk(_lib.BF16, 0, 64) == 0                                      # empty batch
+    assert qk(_lib.BF16, 1, 96) == 2 and b"D must be" in so.dc_last_error()
+    assert qk(_lib.F32, 1, 64) == 1 and b"dtype" in so.dc_last_error()
+    assert qk(_lib.BF16, 1, 64, wdt=_lib.F16) == 1 and b"weight_dtype" in so.dc_last_error()
+    assert qk(_lib.BF16, 1, 64, flags=4) == 1 and b"flags" in so.dc_last_error()
+    assert qk(_lib.BF16, 1, 64, eps=-1.0) == 1 and b"eps" in so.dc_last_error()
 
 
 def test_bench_refuses_more_than_one_gpu():
