@@ -447,3 +447,69 @@ def test_glue_against_the_reference_formulas_in_torch(dtype):
         diff = np.abs(got - want)
         assert (diff == 0).mean() > 0.99
         assert np.all(diff <= ulp * (np.abs(want) + 4.0))
+
+
+# ---------------------------------------------------------------- LayerNorm-modulate + quantize (oracle/quant.py)
+
+def _ln_mod_rows(x, sc1, shift, rows_per_mod, eps, dtype):
+    """The modulated rows the oracle quantizes, recovered by quantizing with
+    group 0 and a scale of 1 would be lossy; instead restate y in float64."""
+    m = np.arange(x.shape[0]) // rows_per_mod
+    x64 = x.astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    var = ((x64 - mu) ** 2).mean(1, keepdims=True)
+    return (x64 - mu) / np.sqrt(var + eps) * sc1[m].astype(np.float64) + shift[m].astype(np.float64)
+
+
+def test_ln_mod_oracle_against_float64_layernorm():
+    """Codes of the oracle equal the codes of the float64 LayerNorm-modulate
+    rounded once to bf16, except where float32 statistics move a value across
+    a bf16 rounding boundary (one step at most, on under 1% of elements)."""
+    g = np.random.default_rng(7)
+    x = (g.standard_normal((12, 512)) * 3 + 1).astype(np.float32)
+    sc1 = OF.round_to(g.uniform(0.5, 1.5, (3, 512)).astype(np.float32), "bf16")
+    sh = OF.round_to(g.standard_normal((3, 512)).astype(np.float32) * 0.1, "bf16")
+    for group in (0, 256):
+        q, s = OQ.ln_mod_quantize(x, sc1, sh, 4, 1e-6, group, "bf16")
+        y = OF.round_to(_ln_mod_rows(x, sc1, sh, 4, 1e-6, "bf16").astype(np.float32), "bf16")
+        q2, s2 = OQ.quantize_activation(y, group)
+        assert np.all(np.abs(q.astype(int) - q2) <= 1) and (q == q2).mean() > 0.99
+        np.testing.assert_allclose(s, s2, rtol=2 ** -7)
+
+
+def _torch_ln_mod_codes(x, sc1, sh, rows_per_mod):
+    """The reference's formula (``_fused.py:73-85``) as torch CPU ops: two-pass
+    float32 mean / variance, ``y = xc * rsqrt(var + eps)``, ``y * sc1 + s``
+    rounded to bf16, then the torch quantizer with ConvRot 256: (codes, scales)."""
+    xt = torch.from_numpy(x)
+    K = x.shape[1]
+    xc = xt - xt.sum(1, keepdim=True) / K
+    y = xc * torch.rsqrt((xc * xc).sum(1, keepdim=True) / K + 1e-6)
+    m = torch.arange(x.shape[0]) // rows_per_mod
+    out = (y * torch.from_numpy(sc1)[m] + torch.from_numpy(sh)[m]).to(torch.bfloat16)
+    q, s = OC.quantize_rows(OC.rotate(out.float(), 256))
+    return q.numpy(), s.numpy()
+
+
+@pytest.mark.parametrize("offset", [0.0, 1000.0])
+def test_ln_mod_oracle_against_torch_statement(offset):
+    """The oracle against torch CPU ops of the reference's formula: codes equal
+    except for float32 order effects (within one step, >99% equal), row scales
+    within 1e-3. Codes are invariant to a per-row factor, so the row scales
+    carry rstd: with a large row mean a planted one-pass variance
+    (E[x^2] - mean^2 in float32) moves them by percents."""
+    g = np.random.default_rng(8)
+    x = (g.standard_normal((16, 768)) + offset).astype(np.float32)
+    sc1 = OF.round_to(g.uniform(0.5, 1.5, (2, 768)).astype(np.float32), "bf16")
+    sh = OF.round_to(g.standard_normal((2, 768)).astype(np.float32) * 0.1, "bf16")
+    qt, st = _torch_ln_mod_codes(x, sc1, sh, 8)
+    q, s = OQ.ln_mod_quantize(x, sc1, sh, 8, 1e-6, 256, "bf16")
+    assert np.all(np.abs(q.astype(int) - qt) <= 1) and (q == qt).mean() > 0.99
+    np.testing.assert_allclose(s, st, rtol=1e-3)
+    if offset:
+        m = np.arange(16) // 8
+        mean32 = x.mean(1, dtype=np.float32, keepdims=True)
+        var1 = (x * x).mean(1, dtype=np.float32, keepdims=True) - mean32 * mean32
+        y1 = ((x - mean32) / np.sqrt(np.maximum(var1, 0) + 1e-6)).astype(np.float32)
+        _, sb = OQ.quantize_activation(OF.round_to(y1 * sc1[m] + sh[m], "bf16"), 256)
+        assert np.abs(sb / st - 1).max() > 1e-2
