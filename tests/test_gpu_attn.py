@@ -140,6 +140,24 @@ def test_deterministic(gpu):
     assert all(torch.equal(outs[0], o) for o in outs[1:])
 
 
+@pytest.mark.parametrize("B,H,L,D,dtype", [(2, 10, 4096, 64, torch.float16), (2, 10, 4096, 64, torch.bfloat16),
+                                             (1, 24, 4096, 128, torch.bfloat16)])
+def test_stream_k_repeat_calls_identical(gpu, B, H, L, D, dtype):
+    """Launches with stream-K pieces and their merge give the same bits on
+    every call (regression: the merge kernel once declared less LDS than its
+    factor / 1 / l / slot layout uses, and tiles merged with another
+    workgroup's factors now and then)."""
+    if A.attn_plan(B, H, L, L, D, dtype)["sk_blocks"] == 0:
+        pytest.skip("no stream-K split at this shape on this device")
+    g = torch.Generator(device=gpu).manual_seed(12)
+    q = torch.randn(B, L, H, D, device=gpu, generator=g).to(dtype)
+    k = (torch.randn(B, L, H, D, device=gpu, generator=g) + 0.5).to(dtype)
+    v = torch.randn(B, L, H, D, device=gpu, generator=g).to(dtype)
+    first = A.int8_attention(q, k, v, D ** -0.5).clone()
+    for _ in range(12):
+        assert torch.equal(A.int8_attention(q, k, v, D ** -0.5), first)
+
+
 def test_stream_k_pieces_match_whole_tiles(gpu):
     """Query tiles past the last whole round of workgroups run as stream-K
     pieces (ranges of key tiles) whose partial O, row maxima and row sums a
