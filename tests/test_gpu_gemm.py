@@ -145,3 +145,17 @@ def test_fused_linears_equal_concatenated_outputs(gpu, bias):
     x = torch.randn(3, 333, 1280, device=gpu, dtype=torch.float16)
     y = fused(x)
     assert torch.equal(y, torch.cat([l(x) for l in layers], -1))
+
+
+@pytest.mark.parametrize("mnk", [(4608, 12288, 3072), (4096, 3072, 3072), (512, 3072, 3072)])
+def test_repeat_calls_identical(gpu, mnk):
+    """The same launch gives the same bits every time (the DMA kernel stages
+    its output through LDS with a cross-lane hand-off; a missing fence there
+    would show as run-to-run differences)."""
+    m, n, k = mnk
+    q, w, sx, sw = _qw(m, n, k, 13)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(13)) * 0.5).to(torch.bfloat16).to(gpu)
+    q, w, sx, sw = q.to(gpu), w.to(gpu), sx.to(gpu), sw.to(gpu)
+    first = _int8._gemm(q, w, sx, sw, bias, torch.bfloat16).clone()
+    for _ in range(8):
+        assert torch.equal(_int8._gemm(q, w, sx, sw, bias, torch.bfloat16), first)
