@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libdiffucore_amd.so"
 
 F16, BF16, F32, I32, NONE = 0, 1, 2, 3, -1
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _DTYPE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int32: I32}
 
@@ -27,7 +27,8 @@ _SIGS = {
     "dc_last_error": (ctypes.c_char_p, []),
     "dc_abi_version": (_I, []),
     "dc_quantize_rows": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _I64, _P, _P]),
-    "dc_w8a8_gemm": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P]),
+    "dc_w8a8_gemm": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, ctypes.c_size_t, _P]),
+    "dc_w8a8_gemm_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
     "dc_w8a8_gemm_plan": (_I, [_I64, _I64, _I64, _I64, _I64]),
     "dc_rescale": (_I, [_P, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P]),
     "dc_ln_mod_quantize_rows": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, ctypes.c_float, _I, _P, _I64, _P, _P]),

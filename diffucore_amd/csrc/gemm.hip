@@ -40,6 +40,10 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int vec_out;  // 1 when 4-wide output stores are aligned
   int vec16;    // 1 when 16-byte output stores at multiples of 16 bytes into a row are aligned
+  // split-K (int32 partials only): blockIdx.y takes k in [y * kslice, (y + 1) * kslice)
+  // and writes its partial sums at out + y * split_stride
+  int ksplit, kslice;
+  int64_t split_stride;
 };
 
 constexpr int BK = 128;            // k bytes per LDS stage
@@ -278,6 +282,15 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], const Ge
 template <class T, int OUT_DT, int BIAS_DT>
 __global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
   constexpr int FN = T::FN, FM = T::FM, NT = T::NT;
+  if constexpr (OUT_DT == DC_I32) {
+    if (p.ksplit > 1) {
+      const int k0 = (int)blockIdx.y * p.kslice;
+      p.a += k0;
+      p.w += k0;
+      p.K = min(p.kslice, p.K - k0);
+      p.out = static_cast<int32_t*>(p.out) + (int64_t)blockIdx.y * p.split_stride;
+    }
+  }
   constexpr int BN = T::BN, BM = T::BM;
   constexpr int CPR = BK / 16;                    // 16-byte chunks per row
   constexpr int NWL = BN * CPR / NT, NAL = BM * CPR / NT;
@@ -603,20 +616,25 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p) {
 #undef DC_WAIT_VMCNT
 #undef DC_WAIT_VMCNT_LGKM0
 
-// Rescale pass over an int32 accumulator (dc_rescale): one thread per 4 outputs.
+// Rescale pass over an int32 accumulator (dc_rescale), or over the sum of
+// nsplit split-K partials split_stride apart (exact in int32): one thread
+// per 4 outputs.
 template <int OUT_DT, int BIAS_DT>
 __global__ void __launch_bounds__(256) rescale_kernel(const int32_t* __restrict__ acc, int64_t lda,
                                                       const float* __restrict__ sx, const float* __restrict__ sw,
                                                       const void* __restrict__ bias, void* __restrict__ out,
-                                                      int64_t ldo, int M, int N) {
+                                                      int64_t ldo, int M, int N, int nsplit, int64_t split_stride) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int n4 = (N + 3) / 4;
   const int64_t m = idx / n4;
   const int n = (int)(idx % n4) * 4;
   if (m >= M) return;
   const float sxm = sx[m];
-  for (int e = 0; e < 4 && n + e < N; ++e)
-    store1<OUT_DT>(out, m * ldo + n + e, epi<OUT_DT, BIAS_DT>(acc[m * lda + n + e], sxm, sw[n + e], bias, n + e));
+  for (int e = 0; e < 4 && n + e < N; ++e) {
+    int32_t a = acc[m * lda + n + e];
+    for (int s = 1; s < nsplit; ++s) a += acc[s * split_stride + m * lda + n + e];
+    store1<OUT_DT>(out, m * ldo + n + e, epi<OUT_DT, BIAS_DT>(a, sxm, sw[n + e], bias, n + e));
+  }
 }
 
 template <class T, int OUT_DT, int BIAS_DT>
@@ -635,7 +653,8 @@ static int launch_gemm(GemmArgs p, hipStream_t st) {
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((w8a8_gemm_kernel<T, OUT_DT, BIAS_DT>), dim3((unsigned)tiles), dim3(T::NT), T::LDS, st, p);
+  const unsigned ks = p.ksplit > 1 ? (unsigned)p.ksplit : 1u;
+  hipLaunchKernelGGL((w8a8_gemm_kernel<T, OUT_DT, BIAS_DT>), dim3((unsigned)tiles, ks), dim3(T::NT), T::LDS, st, p);
   return launch_status("w8a8_gemm_kernel");
 }
 
@@ -714,23 +733,48 @@ static int dispatch_bias(GemmArgs p, int bias_dtype, hipStream_t st) {
 
 template <int OUT_DT, int BIAS_DT>
 static int launch_rescale(const int32_t* acc, int64_t lda, const float* sx, const float* sw, const void* bias,
-                          void* out, int64_t ldo, int64_t M, int64_t N, hipStream_t st) {
+                          void* out, int64_t ldo, int64_t M, int64_t N, hipStream_t st, int nsplit = 1,
+                          int64_t split_stride = 0) {
   const int64_t n = M * ((N + 3) / 4);
   hipLaunchKernelGGL((rescale_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, acc, lda,
-                     sx, sw, bias, out, ldo, (int)M, (int)N);
+                     sx, sw, bias, out, ldo, (int)M, (int)N, nsplit, split_stride);
   return launch_status("rescale_kernel");
 }
 
 template <int OUT_DT>
 static int rescale_bias(const int32_t* acc, int64_t lda, const float* sx, const float* sw, const void* bias,
-                        int bias_dtype, void* out, int64_t ldo, int64_t M, int64_t N, hipStream_t st) {
+                        int bias_dtype, void* out, int64_t ldo, int64_t M, int64_t N, hipStream_t st,
+                        int nsplit = 1, int64_t split_stride = 0) {
   switch (bias_dtype) {
-    case DC_NONE: return launch_rescale<OUT_DT, DC_NONE>(acc, lda, sx, sw, bias, out, ldo, M, N, st);
-    case DC_F16: return launch_rescale<OUT_DT, DC_F16>(acc, lda, sx, sw, bias, out, ldo, M, N, st);
-    case DC_BF16: return launch_rescale<OUT_DT, DC_BF16>(acc, lda, sx, sw, bias, out, ldo, M, N, st);
-    case DC_F32: return launch_rescale<OUT_DT, DC_F32>(acc, lda, sx, sw, bias, out, ldo, M, N, st);
+    case DC_NONE: return launch_rescale<OUT_DT, DC_NONE>(acc, lda, sx, sw, bias, out, ldo, M, N, st, nsplit, split_stride);
+    case DC_F16: return launch_rescale<OUT_DT, DC_F16>(acc, lda, sx, sw, bias, out, ldo, M, N, st, nsplit, split_stride);
+    case DC_BF16: return launch_rescale<OUT_DT, DC_BF16>(acc, lda, sx, sw, bias, out, ldo, M, N, st, nsplit, split_stride);
+    case DC_F32: return launch_rescale<OUT_DT, DC_F32>(acc, lda, sx, sw, bias, out, ldo, M, N, st, nsplit, split_stride);
     default: return fail(DC_EINVAL, "dc_rescale: bad bias_dtype");
   }
+}
+
+// Split-K plan for problems whose 128 x 128 tiles fill at most a quarter of
+// the device's workgroup slots (2 per CU), with K >= 3072 (whatever tile
+// plan_tile would pick for the unsplit call: such problems leave most CUs
+// idle either way; measured, a fuller or shorter problem loses more to the
+// partials' round trip and the second launch than it gains): the largest
+// power of two S <= 8 with S * tiles <= slots and slices of at least 512
+// bytes of k, each slice a multiple of 128. Returns 1 for no split; *kslice
+// is the slice.
+static int splitk_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int* kslice) {
+  *kslice = (int)K;
+  (void)lda; (void)ldw;
+  if (K < 3072) return 1;
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t slots = 2 * (int64_t)device_cus();
+  if (4 * tiles > slots) return 1;
+  int s = 1;
+  while (s < 8 && 2 * s * tiles <= slots && K / (2 * s) >= 512) s *= 2;
+  if (s == 1) return 1;
+  const int64_t slice = ((K + s - 1) / s + 127) / 128 * 128;
+  *kslice = (int)slice;
+  return (int)((K + slice - 1) / slice);
 }
 
 }  // namespace dc
@@ -746,9 +790,17 @@ extern "C" int dc_w8a8_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, i
   return plan_tile(M, N, K, lda, ldw);
 }
 
+extern "C" size_t dc_w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 16 || lda < K || ldw < K || lda % 16 || ldw % 16) return 0;
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return 0;
+  int kslice = 0;
+  const int s = splitk_plan(M, N, K, lda, ldw, &kslice);
+  return s > 1 ? (size_t)s * (size_t)M * (size_t)N * 4 : 0;
+}
+
 extern "C" int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, const float* sx,
                             const float* sw, const void* bias, int bias_dtype, void* out, int out_dtype, int64_t ldo,
-                            int64_t M, int64_t N, int64_t K, void* stream) {
+                            int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
   if (M < 0 || N < 0 || K < 0) return fail(DC_EINVAL, "dc_w8a8_gemm: negative size");
   if (M == 0 || N == 0) return DC_OK;
@@ -769,6 +821,31 @@ extern "C" int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
               (out_dtype == DC_I32 || (reinterpret_cast<uintptr_t>(sw) & 15) == 0);
   p.vec16 = p.vec_out && (reinterpret_cast<uintptr_t>(out) % 16) == 0 && (ldo * ob) % 16 == 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_dtype != DC_I32 && out_dtype != DC_F16 && out_dtype != DC_BF16 && out_dtype != DC_F32)
+    return fail(DC_EINVAL, "dc_w8a8_gemm: bad out_dtype");
+  if (bias_dtype != DC_NONE && bias_dtype != DC_F16 && bias_dtype != DC_BF16 && bias_dtype != DC_F32)
+    return fail(DC_EINVAL, "dc_w8a8_gemm: bad bias_dtype");
+  // split-K into the workspace (int32 partials), then the epilogue over their sum
+  int kslice = 0;
+  const int ks = (out_dtype != DC_I32 && workspace) ? splitk_plan(M, N, K, lda, ldw, &kslice) : 1;
+  if (ks > 1 && ws_bytes >= (size_t)ks * (size_t)M * (size_t)N * 4 && aligned16(workspace)) {
+    GemmArgs q = p;
+    q.sx = nullptr; q.sw = nullptr; q.bias = nullptr;
+    q.out = workspace;
+    q.ldo = N;
+    q.vec_out = N % 4 == 0;
+    q.vec16 = N % 4 == 0;
+    q.ksplit = ks;
+    q.kslice = kslice;
+    q.split_stride = M * N;
+    if (int e = launch_gemm<Tile<2, 2, 2, 2, 1>, DC_I32, DC_NONE>(q, st)) return e;
+    const int32_t* acc = static_cast<const int32_t*>(workspace);
+    switch (out_dtype) {
+      case DC_F16: return rescale_bias<DC_F16>(acc, N, sx, sw, bias, bias_dtype, out, ldo, M, N, st, ks, M * N);
+      case DC_BF16: return rescale_bias<DC_BF16>(acc, N, sx, sw, bias, bias_dtype, out, ldo, M, N, st, ks, M * N);
+      default: return rescale_bias<DC_F32>(acc, N, sx, sw, bias, bias_dtype, out, ldo, M, N, st, ks, M * N);
+    }
+  }
   switch (out_dtype) {
     case DC_I32: return pick_tile<DC_I32, DC_NONE>(p, st);
     case DC_F16: return dispatch_bias<DC_F16>(p, bias_dtype, st);

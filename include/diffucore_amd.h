@@ -139,10 +139,24 @@ int dc_qk_norm_rope(int dtype, int64_t B, int64_t L, int64_t H, int64_t D, int f
  *   Replaces scaled_mm (_int8.py:266-276; kernels/int8_gemm_sm75.cu:75-88)
  *   and int_mm + rescale (_int8.py:313-323), rounding bit for bit like them.
  * Needs K % 16 == 0, lda % 16 == 0, ldw % 16 == 0 and 16-byte aligned a, w.
+ * workspace / ws_bytes (may be NULL / 0): scratch for split-K on problems
+ * whose tiles would leave most of the device idle (small M, long K; see
+ * dc_w8a8_gemm_workspace_bytes). The k range is split over workgroups that
+ * write int32 partial sums there, and an epilogue pass adds them (exact) and
+ * applies the same rescale, bias and cast: results are bit-identical to the
+ * unsplit call. Without enough workspace the call runs unsplit.
  */
 int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, const float* sx,
                  const float* sw, const void* bias, int bias_dtype, void* out, int out_dtype,
-                 int64_t ldo, int64_t M, int64_t N, int64_t K, void* stream);
+                 int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes,
+                 void* stream);
+
+/*
+ * Workspace bytes dc_w8a8_gemm uses for split-K on this problem on the
+ * current device (0: it runs unsplit). No counterpart in the reference, whose
+ * GEMMs are torch._int_mm and one CUTLASS kernel (_int8.py:200-276).
+ */
+size_t dc_w8a8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw);
 
 /*
  * Which GEMM kernel dc_w8a8_gemm runs for a problem on the current device:

@@ -159,3 +159,40 @@ def test_repeat_calls_identical(gpu, mnk):
     first = _int8._gemm(q, w, sx, sw, bias, torch.bfloat16).clone()
     for _ in range(8):
         assert torch.equal(_int8._gemm(q, w, sx, sw, bias, torch.bfloat16), first)
+
+
+def _gemm_unsplit(q, w, sx, sw, bias, dtype):
+    """dc_w8a8_gemm with no workspace (always one pass over k)."""
+    from diffucore_amd import _lib
+    so = _lib.require()
+    M, K = q.shape
+    N = w.shape[0]
+    out = torch.empty(M, N, device=q.device, dtype=dtype)
+    b_p, b_code = (bias.data_ptr(), _lib.dtype_code(bias.dtype)) if bias is not None else (None, _lib.NONE)
+    rc = so.dc_w8a8_gemm(q.data_ptr(), K, w.data_ptr(), K, sx.data_ptr(), sw.data_ptr(), b_p, b_code, out.data_ptr(),
+                         _lib.dtype_code(dtype), N, M, N, K, None, 0, _lib.stream_ptr(q.device))
+    _lib.check(rc, "dc_w8a8_gemm")
+    return out
+
+
+@pytest.mark.parametrize("mnk", [(512, 3072, 12288), (512, 3072, 3072), (154, 640, 4096), (77, 1280, 4096),
+                                 (300, 520, 8192)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_split_k_is_bit_identical(gpu, mnk, dtype):
+    """Small-M, long-K problems split k over workgroups into int32 partials
+    (the FLUX text MLP down, SDXL cross-attention k/v, ...); the epilogue over
+    their exact sum equals the unsplit GEMM and the oracle bit for bit."""
+    from diffucore_amd import _lib
+    m, n, k = mnk
+    ws = _lib.require().dc_w8a8_gemm_workspace_bytes(m, n, k, k, k)
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert ws > 0
+    q, w, sx, sw = _qw(m, n, k, 14)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(14)) * 0.5).to(torch.bfloat16)
+    ref = OG.rescale(OG.int_mm(q.numpy(), w.numpy()), sx.numpy(), sw.numpy(), np32(bias), DT[dtype])
+    q, w, sx, sw, bias = q.to(gpu), w.to(gpu), sx.to(gpu), sw.to(gpu), bias.to(gpu)
+    split = _int8._gemm(q, w, sx, sw, bias, dtype)
+    assert np.array_equal(np32(split).view(np.uint32), ref.view(np.uint32))
+    assert torch.equal(split, _gemm_unsplit(q, w, sx, sw, bias, dtype))
+    for _ in range(4):
+        assert torch.equal(_int8._gemm(q, w, sx, sw, bias, dtype), split)

@@ -199,9 +199,13 @@ def test_argument_checks_fail_before_any_launch():
     assert so.dc_quantize_rows(1, _lib.BF16, 4, 512, 512, 3, 1, 512, 1, None) == 1
     assert b"group" in so.dc_last_error()
     assert so.dc_quantize_rows(1, _lib.BF16, 0, 512, 512, 0, 1, 512, 1, None) == 0      # empty batch
-    assert so.dc_w8a8_gemm(16, 24, 16, 24, 16, 16, None, -1, 16, _lib.BF16, 8, 4, 8, 24, None) == 2
+    assert so.dc_w8a8_gemm(16, 24, 16, 24, 16, 16, None, -1, 16, _lib.BF16, 8, 4, 8, 24, None, 0, None) == 2
     assert b"K" in so.dc_last_error()
-    assert so.dc_w8a8_gemm(16, 32, 16, 32, 16, 16, None, 7, 16, _lib.BF16, 8, 4, 8, 32, None) == 1
+    assert so.dc_w8a8_gemm(16, 32, 16, 32, 16, 16, None, 7, 16, _lib.BF16, 8, 4, 8, 32, None, 0, None) == 1
+    # split-K workspace: small M with long K splits (FLUX text MLP down: 4 slices of int32 partials), big M does not
+    assert so.dc_w8a8_gemm_workspace_bytes(512, 3072, 12288, 12288, 12288) == 4 * 512 * 3072 * 4
+    assert so.dc_w8a8_gemm_workspace_bytes(4096, 3072, 12288, 12288, 12288) == 0
+    assert so.dc_w8a8_gemm_workspace_bytes(512, 3072, 100, 112, 112) == 0
     assert so.dc_int8_attn_workspace_bytes(1, 24, 4608, 4608, 128) > 24 * 4608 * 128
     assert so.dc_int8_attn_workspace_bytes(1, 1, 1, 1, 200) == 0
     st = (_lib.ctypes.c_int64 * 3)(8, 8, 8)
