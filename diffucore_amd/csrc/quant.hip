@@ -12,8 +12,9 @@
 // workgroups and reduce segment maxima through LDS. The loads of a lane are
 // all issued before any is used, and the many short wave tasks let late loads
 // overlap early arithmetic. The arithmetic per element (rotation, absmax,
-// code) is about 20 VALU instructions: at FLUX shapes the kernel is bound by
-// VALU issue and the HBM stream together.
+// code) is about 15 VALU instructions (unpack 1, butterfly 8.5, absmax 0.5,
+// code 4, packing 0.75): at FLUX shapes the kernel is bound by VALU issue
+// and the HBM stream together.
 //
 // ConvRot (group 256): x @ H_256 with H_256 = H4 (x) H4 (x) H4 (x) H4 / 16.
 // The in-group index i = 64*d1 + 16*d2 + 4*d3 + d4 is split so that the
@@ -47,6 +48,51 @@ __device__ __forceinline__ void h4(float& x0, float& x1, float& x2, float& x3) {
   x0 = y0; x1 = y1; x2 = y2; x3 = y3;
 }
 
+// H4 across the 4 lanes of each quad (lane bits 0, 1), for 8 values per lane:
+// pair = x[l^1] + x[l], s = pair[l^2] + pair[l], y = s + x[l^3] * -2, the
+// same operations in the same order as h4 (with the lanes of a quad in the
+// roles of x0..x3), three DPP instructions per value. The compiler folds
+// only some DPP moves into their users and cannot fold one into the FMA,
+// whose -2 must then sit in a register: written out, the step takes 3
+// instructions per value instead of 5. s_nop 1 before each group keeps two
+// wait states between a VALU write and a DPP read of that register (the
+// first group reads values written before the block).
+__device__ __forceinline__ void h4_quad8(float (&x)[8]) {
+  float p[8];
+  const float m2 = -2.0f;
+  asm volatile(
+      "s_nop 1\n"
+      "v_add_f32_dpp %0, %8, %8 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %1, %9, %9 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %2, %10, %10 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %3, %11, %11 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %4, %12, %12 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %5, %13, %13 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %6, %14, %14 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %7, %15, %15 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "s_nop 1\n"
+      "v_add_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %1, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %2, %2, %2 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %3, %3, %3 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %4, %4, %4 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %5, %5, %5 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %6, %6, %6 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_add_f32_dpp %7, %7, %7 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %0, %8, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %1, %9, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %2, %10, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %3, %11, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %4, %12, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %5, %13, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %6, %14, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      "v_fmac_f32_dpp %7, %15, %16 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+      : "=&v"(p[0]), "=&v"(p[1]), "=&v"(p[2]), "=&v"(p[3]), "=&v"(p[4]), "=&v"(p[5]), "=&v"(p[6]), "=&v"(p[7])
+      : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(m2));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = p[e];
+}
+
 // 16 * (x @ H_256) of the lane's 256-group, in place.
 // v[j][e]: element 64*j + 8*q8 + e of the lane's 256-group, q8 = 2*d2 + d3hi,
 // with d2 = lane & 3 and d3hi = (lane >> 2) & 1.
@@ -54,16 +100,9 @@ __device__ __forceinline__ void hadamard256(float (&v)[4][8]) {
   // d1: across the 4 chunks
 #pragma unroll
   for (int e = 0; e < 8; ++e) h4(v[0][e], v[1][e], v[2][e], v[3][e]);
-  // d2: lanes l, l^1, l^2, l^3 (quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, [3,2,1,0] = 0x1B)
+  // d2: lanes l, l^1, l^2, l^3
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = v[j][e];
-      const float pair = x + dpp<0xB1>(x);
-      const float s = pair + dpp<0x4E>(pair);
-      v[j][e] = s_minus_2x(s, dpp<0x1B>(x));
-    }
+  for (int j = 0; j < 4; ++j) h4_quad8(v[j]);
   // d3 = 2*d3hi + (e >> 2): partner lane l^4 holds the other d3hi
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -88,29 +127,27 @@ __device__ __forceinline__ void hadamard256(float (&v)[4][8]) {
 // ---------------------------------------------------------------- int8 codes
 //
 // The reference's code is clamp(rint(fl(x / s)), -128, 127) with an IEEE
-// division. Here every |x| <= amax and s >= fl(amax / 127), so |x / s| <=
-// 127 (1 + 2^-23) and the clamp never acts. With inv = fl(1 / s) (once per
-// row), the exact product u = x * inv and fl(x / s) both lie within
-// |x / s| * 2^-24 of x / s. fma(x, inv, 1.5 * 2^23) rounds u to an integer n
-// (ties to even), its low byte being the two's complement code, and
-// fma(x, inv, -n) gives u - n to within 2^-26. Unless u lies within
-// (|n| + 1) * 2^-22 - 2^-24 (> |u - fl(x / s)|) of a half-integer, u and
-// fl(x / s) round to the same integer. A lane holding an element inside that
-// window (about 1e-5 of random elements) redoes its codes with the division.
+// division. Every |x| <= amax and s >= fl(amax / 127), so |fl(x / s)| <= 127
+// and the clamp never acts. The quotient is formed without a division by
+// Markstein's correction (P. Markstein, IBM J. Res. Dev. 34(1), 1990; the
+// quotient-correction theorem in Muller et al., Handbook of Floating-Point
+// Arithmetic): with y = fl(1 / s) correctly rounded (one IEEE division per
+// row) and q = fl(x * y), within one ulp of x / s, the residual
+// r = fma(-q, s, x) is exact and fma(r, y, q) = fl(x / s), correctly rounded,
+// unless something underflows. An inexact residual needs |x| < 2^-103, and
+// s >= 1e-30 then puts |x / s| below 0.1: the code is 0 either way. Adding
+// 1.5 * 2^23 rounds the quotient to an integer (ties to even) whose low byte
+// is the two's complement code: mul, fma, fma, add per element.
 //
 // After the rotation the values still carry the butterfly's factor 16: the
-// kernels fold the exact 1/16 into amax and inv (a power-of-two scaling is
-// exact above 2^-122; below, the code is 0 either way) and apply it to x only
-// on the division path.
+// kernels fold the exact 1/16 into y and the 16 into s for the residual, so
+// each product and residual is the unscaled one times a power of two.
 constexpr float QMAGIC = 12582912.0f;              // 1.5 * 2^23
-constexpr float NEAR_HALF = 0.49999976158142090f;  // 0.5 - 2^-22
-constexpr float NEAR_SLOPE = 2.384185791015625e-07f;  // 2^-22
 
-__device__ __forceinline__ uint32_t code_fast(float x, float inv, bool& near) {
-  const float y = __builtin_fmaf(x, inv, QMAGIC);
-  const float n = y - QMAGIC;
-  near |= __builtin_fmaf(fabsf(n), NEAR_SLOPE, fabsf(__builtin_fmaf(x, inv, -n))) >= NEAR_HALF;
-  return __float_as_uint(y);
+__device__ __forceinline__ uint32_t code_of(float x, float y, float s) {
+  const float q = x * y;
+  const float r = __builtin_fmaf(-q, s, x);
+  return __float_as_uint(__builtin_fmaf(r, y, q) + QMAGIC);
 }
 
 __device__ __forceinline__ uint32_t code_exact(float x, float s) {
@@ -130,41 +167,19 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, ui
 template <int NG, int PRE>
 __device__ __forceinline__ void quantize_store(const float (&v)[NG][4][8], const bool (&ok)[NG][4],
                                                const int (&off)[NG][4], float s, int8_t* qrow) {
-  constexpr float unpre = 1.0f / PRE;
-  const float inv = (1.0f / s) * unpre;
-  bool near = false;
-  uint32_t w[NG][4][2];
+  const float y = (1.0f / s) * (1.0f / PRE), sp = s * (float)PRE;
 #pragma unroll
   for (int n = 0; n < NG; ++n)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const float* e = &v[n][j][4 * h];
-        const uint32_t a = code_fast(e[0], inv, near), b = code_fast(e[1], inv, near);
-        const uint32_t c = code_fast(e[2], inv, near), d = code_fast(e[3], inv, near);
-        w[n][j][h] = pack4(a, b, c, d);
+        w[h] = pack4(code_of(e[0], y, sp), code_of(e[1], y, sp), code_of(e[2], y, sp), code_of(e[3], y, sp));
       }
-#pragma unroll
-  for (int n = 0; n < NG; ++n)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (ok[n][j]) *reinterpret_cast<uint2*>(qrow + off[n][j]) = make_uint2(w[n][j][0], w[n][j][1]);
-  // Rare: redo this lane's codes with the division and store them again. The
-  // stores keep the compiler from evaluating the divisions unconditionally.
-  if (near) {
-#pragma unroll
-    for (int n = 0; n < NG; ++n)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float* e = &v[n][j][0];
-        const uint32_t lo = pack4(code_exact(e[0] * unpre, s), code_exact(e[1] * unpre, s),
-                                  code_exact(e[2] * unpre, s), code_exact(e[3] * unpre, s));
-        const uint32_t hi = pack4(code_exact(e[4] * unpre, s), code_exact(e[5] * unpre, s),
-                                  code_exact(e[6] * unpre, s), code_exact(e[7] * unpre, s));
-        if (ok[n][j]) *reinterpret_cast<uint2*>(qrow + off[n][j]) = make_uint2(lo, hi);
-      }
-  }
+      if (ok[n][j]) *reinterpret_cast<uint2*>(qrow + off[n][j]) = make_uint2(w[0], w[1]);
+    }
 }
 
 // scale = max(amax / 127, 1e-30) from the absmax of PRE-scaled values
@@ -200,7 +215,9 @@ __device__ __forceinline__ void unpack8(const uint4 (&r)[DT == DC_F32 ? 2 : 1], 
 // Group g0 + units * n (n < NG) of the row for the lane's unit g0 < units.
 // Every load is issued, unconditionally, before any is used: chunks past the
 // row (or of idle lanes) read the row's first chunk and are zeroed after.
-template <int DT, int NG>
+// ZERO = false leaves the chunks of idle lanes as loaded (for kernels whose
+// idle lanes' results are never read).
+template <int DT, int NG, bool ZERO = true>
 __device__ __forceinline__ void load_groups(const void* x, int64_t rowoff, int K, int g0, int units, int q8,
                                             float (&v)[NG][4][8], bool (&ok)[NG][4], int (&off)[NG][4]) {
   constexpr int NQ = DT == DC_F32 ? 2 : 1;
@@ -220,7 +237,7 @@ __device__ __forceinline__ void load_groups(const void* x, int64_t rowoff, int K
 #pragma unroll
   for (int n = 0; n < NG; ++n)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) unpack8<DT>(raw[n][j], ok[n][j], v[n][j]);
+    for (int j = 0; j < 4; ++j) unpack8<DT>(raw[n][j], ZERO ? ok[n][j] : true, v[n][j]);
 }
 
 template <int NG>
@@ -295,7 +312,9 @@ __global__ void __launch_bounds__(1024) quant_rows_lds_kernel(const void* __rest
   float v[1][4][8];
   bool ok[1][4];
   int off[1][4];
-  load_groups<DT, 1>(x, (live ? row : 0) * ldx, K, li >> 3, live ? G : 0, q8, v, ok, off);
+  // lanes without a live row compute on row 0's values unzeroed: their
+  // segment maxima fill only their own slots of red, which no live row reads
+  load_groups<DT, 1, false>(x, (live ? row : 0) * ldx, K, li >> 3, live ? G : 0, q8, v, ok, off);
   if constexpr (ROT) hadamard256(v[0]);
   const float seg = seg_max<S>(lane_amax(v));
   if ((t & (S - 1)) == 0) red[t / S] = seg;
