@@ -13,8 +13,9 @@
 // the eager torch ops and the reference's Triton kernel (fp fusion off) do.
 //
 // One row (a token's head, D elements) goes to D/8 lanes, 8 consecutive
-// elements per lane: one 16-byte load, a sum of squares reduced by xor
-// shuffles inside the row's lanes, 16-byte stores. A workgroup of 256 threads
+// elements per lane: one 16-byte load, a sum of squares reduced across the
+// row's lanes by DPP steps, 16-byte stores. Each lane issues all its loads
+// (row, weights, rotary matrices) before any arithmetic. A workgroup of 256 threads
 // takes 256/(D/8) rows. q, k and an optional plain copy of v (to gather two
 // streams' v into one buffer for the attention) run in one launch, one
 // contiguous range of workgroups each. The kernel is bound by HBM: 2 bytes
@@ -74,6 +75,39 @@ __device__ __forceinline__ float rot(float f0, float a, float f1, float b) {
   return p + q;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float qk_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int PATTERN>
+__device__ __forceinline__ float qk_swz(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), PATTERN));
+}
+
+// Sum over the LPR lanes of a row (aligned groups of LPR lanes), the same
+// value in every lane: quad steps (lane ^ 1, lane ^ 2), then the mirrored
+// lane within 8 (row_half_mirror) and within 16 (row_mirror), then lane ^ 16
+// (ds_swizzle). Each step adds two equal partial sums, so all lanes agree bit
+// for bit; DPP steps cost a VALU op, not an LDS round trip.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+  v += qk_dpp<0xB1>(v);                                // quad_perm [1,0,3,2]
+  v += qk_dpp<0x4E>(v);                                // quad_perm [2,3,0,1]
+  if constexpr (LPR >= 8) v += qk_dpp<0x141>(v);       // row_half_mirror
+  if constexpr (LPR >= 16) v += qk_dpp<0x140>(v);      // row_mirror
+  if constexpr (LPR >= 32) v += qk_swz<0x401F>(v);     // lane ^ 16 (and 0x1f, xor 0x10)
+  return v;
+}
+
+// The value of lane j ^ (LPR / 2) of the same row.
+template <int LPR>
+__device__ __forceinline__ float partner(float v) {
+  if constexpr (LPR == 4) return qk_dpp<0x4E>(v);       // lane ^ 2
+  else if constexpr (LPR == 8) return qk_swz<0x101F>(v);   // lane ^ 4
+  else if constexpr (LPR == 16) return qk_dpp<0x128>(v);   // row_ror:8 = lane ^ 8 within 16
+  else return qk_swz<0x401F>(v);                        // lane ^ 16
+}
+
 template <int DT, int LPR>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
   constexpr int RPW = 256 / LPR;
@@ -81,7 +115,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
   const int blk = blockIdx.x - side * a.blocks_per_side;
   const int row = blk * RPW + (int)threadIdx.x / LPR;
   const int j = (int)threadIdx.x % LPR;
-  if (row >= a.rows) return;  // whole rows leave together: the shuffles stay inside live rows
+  if (row >= a.rows) return;  // whole rows leave together: the lane exchanges stay inside live rows
   const QKSide s = side == 0 ? a.s0 : (side == 1 ? a.s1 : a.s2);
   const int h = row % a.H;
   const int bl = row / a.H;
@@ -93,23 +127,48 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
     *reinterpret_cast<uint4*>(dst) = raw;
     return;
   }
+  // every load before any arithmetic: the weights, then the lane's rotary
+  // matrices (pairs 4j .. 4j + 3 for adjacent pairs; for half pairs the 8
+  // pairs of the lane's first-half position, shared with its partner lane)
+  const bool rope = a.freqs != nullptr, half = (a.flags & DC_QK_ROPE_HALF) != 0;
+  const bool lo = j < LPR / 2;
+  uint4 wraw[2];
+  if (a.w_f32) {
+    const uint4* wp = reinterpret_cast<const uint4*>(static_cast<const float*>(s.w) + j * 8);
+    wraw[0] = wp[0];
+    wraw[1] = wp[1];
+  } else {
+    wraw[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(s.w) + j * 8);
+    wraw[1] = wraw[0];
+  }
+  float4 fq[8];
+  if (rope) {
+    const float4* f = reinterpret_cast<const float4*>(a.freqs + b * a.fb + l * a.fl);
+    if (half) {
+      const int pj = lo ? j : j - LPR / 2;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) fq[i] = f[pj * 8 + i];
+    } else {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) fq[p] = f[j * 4 + p];
+    }
+  }
+
   float x[8];
   unpack8<DT>(raw, x);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += materialize(x[i] * x[i]);
-#pragma unroll
-  for (int o = LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  ss = row_sum<LPR>(ss);
   const float r = rsqrtf(ss * a.inv_d + a.eps);
 
   float w[8];
   if (a.w_f32) {
-    const float4* wp = reinterpret_cast<const float4*>(static_cast<const float*>(s.w) + j * 8);
-    const float4 w0 = wp[0], w1 = wp[1];
-    w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
-    w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
+    const uint32_t wv[8] = {wraw[0].x, wraw[0].y, wraw[0].z, wraw[0].w, wraw[1].x, wraw[1].y, wraw[1].z, wraw[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = __uint_as_float(wv[i]);
   } else {
-    unpack8<DT>(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(s.w) + j * 8), w);
+    unpack8<DT>(wraw[0], w);
   }
   float n[8];
   if (a.flags & DC_QK_WEIGHT_F32) {
@@ -120,26 +179,22 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
     for (int i = 0; i < 8; ++i) n[i] = rnd<DT>(rnd<DT>(x[i] * r) * w[i]);
   }
 
-  if (a.freqs != nullptr) {
-    const float* f = a.freqs + b * a.fb + l * a.fl;
+  if (rope) {
     float o[8];
-    if (a.flags & DC_QK_ROPE_HALF) {
+    if (half) {
       // pair (i, i + D/2): lane j < LPR/2 holds the first halves, lane j ^ LPR/2 the second
-      float m[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) m[i] = __shfl_xor(n[i], LPR / 2);
-      const bool lo = j < LPR / 2;
-      const float4* fp = reinterpret_cast<const float4*>(f) + (lo ? j : j - LPR / 2) * 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float4 c = fp[i];
-        o[i] = lo ? rot(c.x, n[i], c.y, m[i]) : rot(c.z, m[i], c.w, n[i]);
+        const float m = partner<LPR>(n[i]);
+        const float4 c = fq[i];
+        // selects, not branches: the lower lane takes row 0 of the matrix, the upper row 1
+        const float a0 = lo ? n[i] : m, b0 = lo ? m : n[i];
+        o[i] = rot(lo ? c.x : c.z, a0, lo ? c.y : c.w, b0);
       }
     } else {
-      const float4* fp = reinterpret_cast<const float4*>(f) + j * 4;
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
-        const float4 c = fp[p];
+        const float4 c = fq[p];
         o[2 * p] = rot(c.x, n[2 * p], c.y, n[2 * p + 1]);
         o[2 * p + 1] = rot(c.z, n[2 * p], c.w, n[2 * p + 1]);
       }
