@@ -637,6 +637,42 @@ __global__ void __launch_bounds__(256) rescale_kernel(const int32_t* __restrict_
   }
 }
 
+// The same pass four outputs at a time with 16-byte partial loads and one
+// 8- or 16-byte store, when N, lda, ldo and split_stride are multiples of 4
+// and acc and out are aligned to match (the split-K workspace always is).
+// Each output is rounded by the same epi() as above.
+template <int OUT_DT, int BIAS_DT>
+__global__ void __launch_bounds__(256) rescale_vec_kernel(const int32_t* __restrict__ acc, int64_t lda,
+                                                          const float* __restrict__ sx, const float* __restrict__ sw,
+                                                          const void* __restrict__ bias, void* __restrict__ out,
+                                                          int64_t ldo, int M, int N, int nsplit,
+                                                          int64_t split_stride) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int n4 = N / 4;
+  const int64_t m = idx / n4;
+  const int n = (int)(idx % n4) * 4;
+  if (m >= M) return;
+  const int4* src = reinterpret_cast<const int4*>(acc + m * lda + n);
+  int4 a = src[0];
+  for (int s = 1; s < nsplit; ++s) {
+    const int4 b = src[s * (split_stride / 4)];
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  }
+  const float sxm = sx[m];
+  const float4 s4 = *reinterpret_cast<const float4*>(sw + n);
+  const float y0 = epi<OUT_DT, BIAS_DT>(a.x, sxm, s4.x, bias, n);
+  const float y1 = epi<OUT_DT, BIAS_DT>(a.y, sxm, s4.y, bias, n + 1);
+  const float y2 = epi<OUT_DT, BIAS_DT>(a.z, sxm, s4.z, bias, n + 2);
+  const float y3 = epi<OUT_DT, BIAS_DT>(a.w, sxm, s4.w, bias, n + 3);
+  if constexpr (OUT_DT == DC_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(out) + m * ldo + n) = make_float4(y0, y1, y2, y3);
+  } else {
+    const uint32_t lo = f32_to_h16<OUT_DT>(y0) | (f32_to_h16<OUT_DT>(y1) << 16);
+    const uint32_t hi = f32_to_h16<OUT_DT>(y2) | (f32_to_h16<OUT_DT>(y3) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + m * ldo + n) = make_uint2(lo, hi);
+  }
+}
+
 template <class T, int OUT_DT, int BIAS_DT>
 static int launch_gemm(GemmArgs p, hipStream_t st) {
   p.tiles_n = (p.N + T::BN - 1) / T::BN;
@@ -735,6 +771,14 @@ template <int OUT_DT, int BIAS_DT>
 static int launch_rescale(const int32_t* acc, int64_t lda, const float* sx, const float* sw, const void* bias,
                           void* out, int64_t ldo, int64_t M, int64_t N, hipStream_t st, int nsplit = 1,
                           int64_t split_stride = 0) {
+  const int ob = OUT_DT == DC_F32 ? 4 : 2;
+  if (N % 4 == 0 && lda % 4 == 0 && ldo % 4 == 0 && split_stride % 4 == 0 && aligned16(acc) && aligned16(sw) &&
+      reinterpret_cast<uintptr_t>(out) % (4 * ob) == 0) {
+    const int64_t n = M * (N / 4);
+    hipLaunchKernelGGL((rescale_vec_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       acc, lda, sx, sw, bias, out, ldo, (int)M, (int)N, nsplit, split_stride);
+    return launch_status("rescale_vec_kernel");
+  }
   const int64_t n = M * ((N + 3) / 4);
   hipLaunchKernelGGL((rescale_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, acc, lda,
                      sx, sw, bias, out, ldo, (int)M, (int)N, nsplit, split_stride);
