@@ -66,6 +66,23 @@ def test_bias_double_rounding(gpu, dtype, bias_dtype):
     assert torch.equal(out, two)
 
 
+@pytest.mark.parametrize("pad", [1, 4])
+def test_rescale_strided_accumulator(gpu, pad):
+    """dc_rescale on a row-strided int32 view (row stride N + pad: the one-
+    output-per-thread pass for pad 1, the four-output pass for pad 4) equals
+    the same values laid out contiguously, and the oracle."""
+    q, w, sx, sw = _qw(257, 516, 512, 12)
+    acc = _int8.int_mm(q.to(gpu), w.to(gpu))
+    big = torch.zeros(257, 516 + pad, device=gpu, dtype=torch.int32)
+    big[:, :516] = acc
+    bias = (torch.randn(516) * 0.5).to(torch.bfloat16).to(gpu)
+    got = _int8.rescale(big[:, :516], sx.to(gpu), sw.to(gpu), bias, torch.bfloat16)
+    want = _int8.rescale(acc, sx.to(gpu), sw.to(gpu), bias, torch.bfloat16)
+    assert torch.equal(got, want)
+    ref = OG.rescale(acc.cpu().numpy(), sx.numpy(), sw.numpy(), np32(bias), DT[torch.bfloat16])
+    assert np.array_equal(np32(got).view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("k,n,group", [(2048, 2048, 256), (768, 512, 256), (1024, 8192, 256), (320, 1280, 0)])
 def test_int8_linear_matches_oracle_and_float(gpu, k, n, group):
     torch.manual_seed(4)
