@@ -14,9 +14,11 @@
 //
 // One row (a token's head, D elements) goes to D/8 lanes, 8 consecutive
 // elements per lane: one 16-byte load, a sum of squares reduced across the
-// row's lanes by DPP steps, 16-byte stores. Each lane issues all its loads
-// (row, weights, rotary matrices) before any arithmetic. A workgroup of 256 threads
-// takes 256/(D/8) rows. q, k and an optional plain copy of v (to gather two
+// row's lanes by DPP steps, 16-byte stores. A lane group takes up to 4 heads
+// of one token, so the weights and the token's rotary matrices are read once
+// for all of them, and each lane issues all its loads before any arithmetic.
+// A workgroup of 256 threads takes 256/(D/8) lane groups. q, k and an
+// optional plain copy of v (to gather two
 // streams' v into one buffer for the attention) run in one launch, one
 // contiguous range of workgroups each. The kernel is bound by HBM: 2 bytes
 // read and 2 written per element, the weights and the frequency rows come
@@ -108,23 +110,30 @@ __device__ __forceinline__ float partner(float v) {
   else return qk_swz<0x401F>(v);                        // lane ^ 16
 }
 
-template <int DT, int LPR>
+// NH consecutive heads of one token per lane group (H % NH == 0): the
+// weights and the token's rotary matrices are loaded once for all of them.
+template <int DT, int LPR, int NH>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
-  constexpr int RPW = 256 / LPR;
+  constexpr int RPW = 256 / LPR;   // lane groups per workgroup
   const int side = blockIdx.x / a.blocks_per_side;
   const int blk = blockIdx.x - side * a.blocks_per_side;
-  const int row = blk * RPW + (int)threadIdx.x / LPR;
+  const int grp = blk * RPW + (int)threadIdx.x / LPR;   // rows NH * grp .. NH * grp + NH - 1
   const int j = (int)threadIdx.x % LPR;
-  if (row >= a.rows) return;  // whole rows leave together: the lane exchanges stay inside live rows
+  if (grp * NH >= a.rows) return;  // whole groups leave together: the lane exchanges stay inside live rows
   const QKSide s = side == 0 ? a.s0 : (side == 1 ? a.s1 : a.s2);
-  const int h = row % a.H;
-  const int bl = row / a.H;
+  const int row0 = grp * NH;
+  const int h0 = row0 % a.H;
+  const int bl = row0 / a.H;
   const int l = bl % a.L;
   const int b = bl / a.L;
-  const uint4 raw = *reinterpret_cast<const uint4*>(s.x + b * s.sx0 + l * s.sx1 + h * s.sx2 + j * 8);
-  uint16_t* dst = s.out + b * s.so0 + l * s.so1 + h * s.so2 + j * 8;
+  const uint16_t* src = s.x + b * s.sx0 + l * s.sx1 + h0 * s.sx2 + j * 8;
+  uint16_t* dst = s.out + b * s.so0 + l * s.so1 + h0 * s.so2 + j * 8;
+  uint4 raw[NH];
+#pragma unroll
+  for (int r = 0; r < NH; ++r) raw[r] = *reinterpret_cast<const uint4*>(src + r * s.sx2);
   if (s.w == nullptr) {
-    *reinterpret_cast<uint4*>(dst) = raw;
+#pragma unroll
+    for (int r = 0; r < NH; ++r) *reinterpret_cast<uint4*>(dst + r * s.so2) = raw[r];
     return;
   }
   // every load before any arithmetic: the weights, then the lane's rotary
@@ -153,15 +162,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
       for (int p = 0; p < 4; ++p) fq[p] = f[j * 4 + p];
     }
   }
-
-  float x[8];
-  unpack8<DT>(raw, x);
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss += materialize(x[i] * x[i]);
-  ss = row_sum<LPR>(ss);
-  const float r = rsqrtf(ss * a.inv_d + a.eps);
-
   float w[8];
   if (a.w_f32) {
     const uint32_t wv[8] = {wraw[0].x, wraw[0].y, wraw[0].z, wraw[0].w, wraw[1].x, wraw[1].y, wraw[1].z, wraw[1].w};
@@ -170,56 +170,74 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
   } else {
     unpack8<DT>(wraw[0], w);
   }
-  float n[8];
-  if (a.flags & DC_QK_WEIGHT_F32) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) n[i] = rnd<DT>(w[i] * materialize(x[i] * r));
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) n[i] = rnd<DT>(rnd<DT>(x[i] * r) * w[i]);
-  }
 
-  if (rope) {
-    float o[8];
-    if (half) {
-      // pair (i, i + D/2): lane j < LPR/2 holds the first halves, lane j ^ LPR/2 the second
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float m = partner<LPR>(n[i]);
-        const float4 c = fq[i];
-        // selects, not branches: the lower lane takes row 0 of the matrix, the upper row 1
-        const float a0 = lo ? n[i] : m, b0 = lo ? m : n[i];
-        o[i] = rot(lo ? c.x : c.z, a0, lo ? c.y : c.w, b0);
-      }
+  for (int r = 0; r < NH; ++r) {
+    float x[8];
+    unpack8<DT>(raw[r], x);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += materialize(x[i] * x[i]);
+    ss = row_sum<LPR>(ss);
+    const float rr = rsqrtf(ss * a.inv_d + a.eps);
+    float n[8];
+    if (a.flags & DC_QK_WEIGHT_F32) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) n[i] = rnd<DT>(w[i] * materialize(x[i] * rr));
     } else {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const float4 c = fq[p];
-        o[2 * p] = rot(c.x, n[2 * p], c.y, n[2 * p + 1]);
-        o[2 * p + 1] = rot(c.z, n[2 * p], c.w, n[2 * p + 1]);
-      }
+      for (int i = 0; i < 8; ++i) n[i] = rnd<DT>(rnd<DT>(x[i] * rr) * w[i]);
     }
-    *reinterpret_cast<uint4*>(dst) = pack8<DT>(o);
-  } else {
-    *reinterpret_cast<uint4*>(dst) = pack8<DT>(n);
+    if (rope) {
+      float o[8];
+      if (half) {
+        // pair (i, i + D/2): lane j < LPR/2 holds the first halves, lane j ^ LPR/2 the second
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float m = partner<LPR>(n[i]);
+          const float4 c = fq[i];
+          // selects, not branches: the lower lane takes row 0 of the matrix, the upper row 1
+          const float a0 = lo ? n[i] : m, b0 = lo ? m : n[i];
+          o[i] = rot(lo ? c.x : c.z, a0, lo ? c.y : c.w, b0);
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float4 c = fq[p];
+          o[2 * p] = rot(c.x, n[2 * p], c.y, n[2 * p + 1]);
+          o[2 * p + 1] = rot(c.z, n[2 * p], c.w, n[2 * p + 1]);
+        }
+      }
+      *reinterpret_cast<uint4*>(dst + r * s.so2) = pack8<DT>(o);
+    } else {
+      *reinterpret_cast<uint4*>(dst + r * s.so2) = pack8<DT>(n);
+    }
   }
 }
 
-template <int DT, int LPR>
+template <int DT, int LPR, int NH>
 static int launch_qk(QKArgs& a, int nsides, hipStream_t st) {
   constexpr int RPW = 256 / LPR;
-  a.blocks_per_side = (a.rows + RPW - 1) / RPW;
-  hipLaunchKernelGGL((qk_norm_rope_kernel<DT, LPR>), dim3(a.blocks_per_side * nsides), dim3(256), 0, st, a);
+  const int groups = a.rows / NH;   // H % NH == 0, so rows % NH == 0
+  a.blocks_per_side = (groups + RPW - 1) / RPW;
+  hipLaunchKernelGGL((qk_norm_rope_kernel<DT, LPR, NH>), dim3(a.blocks_per_side * nsides), dim3(256), 0, st, a);
   return launch_status("dc_qk_norm_rope");
+}
+
+template <int DT, int LPR>
+static int launch_qk_heads(QKArgs& a, int nsides, hipStream_t st) {
+  if (a.H % 4 == 0) return launch_qk<DT, LPR, 4>(a, nsides, st);
+  if (a.H % 2 == 0) return launch_qk<DT, LPR, 2>(a, nsides, st);
+  return launch_qk<DT, LPR, 1>(a, nsides, st);
 }
 
 template <int DT>
 static int dispatch_qk(QKArgs& a, int D, int nsides, hipStream_t st) {
   switch (D) {
-    case 32: return launch_qk<DT, 4>(a, nsides, st);
-    case 64: return launch_qk<DT, 8>(a, nsides, st);
-    case 128: return launch_qk<DT, 16>(a, nsides, st);
-    default: return launch_qk<DT, 32>(a, nsides, st);
+    case 32: return launch_qk_heads<DT, 4>(a, nsides, st);
+    case 64: return launch_qk_heads<DT, 8>(a, nsides, st);
+    case 128: return launch_qk_heads<DT, 16>(a, nsides, st);
+    default: return launch_qk_heads<DT, 32>(a, nsides, st);
   }
 }
 
