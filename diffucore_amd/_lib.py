@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libdiffucore_amd.so"
 
 F16, BF16, F32, I32, NONE = 0, 1, 2, 3, -1
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _DTYPE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int32: I32}
 

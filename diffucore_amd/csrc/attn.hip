@@ -32,6 +32,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace dc {
 
@@ -765,21 +766,24 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs p) {
 // ---------------------------------------------------------------- host
 
 // Attention workgroups resident at once on the current device (occupancy x
-// CUs, cached per device); 2 per CU on 256 CUs when no device answers.
+// CUs, cached per device; concurrent first calls store the same value); 2 per
+// CU on 256 CUs when no device answers.
 template <int DT, int DP>
 static int attn_slots() {
-  static int slots[64] = {0};
+  static std::atomic<int> slots[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
-  if (!slots[dev]) {
+  int n = slots[dev].load(std::memory_order_relaxed);
+  if (!n) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&attn_kernel<DT, DP>),
                                                      256, 0) != hipSuccess || per_cu <= 0)
       per_cu = 2;
-    slots[dev] = cus * per_cu;
+    n = cus * per_cu;
+    slots[dev].store(n, std::memory_order_relaxed);
   }
-  return slots[dev];
+  return n;
 }
 
 // Work split (AttnArgs::dp_blocks / sk_blocks / sk_tiles). Query tiles fill

@@ -26,6 +26,8 @@
 // deals workgroups round-robin over them) works a contiguous, L2-friendly range.
 #include "common.h"
 
+#include <atomic>
+
 namespace dc {
 
 struct GemmArgs {
@@ -679,15 +681,19 @@ static int launch_gemm(GemmArgs p, hipStream_t st) {
   p.tiles_m = (p.M + T::BM - 1) / T::BM;
   const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
   if (tiles > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm: problem too large");
-  static bool attr_set = false;   // per instantiation; the attribute is process-wide
-  if (!attr_set) {
+  // the LDS attribute, set once per instantiation and device; threads that
+  // race on a first call each set it (the call is idempotent)
+  static std::atomic<bool> attr_set[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w8a8_gemm_kernel<T, OUT_DT, BIAS_DT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS);
     if (e != hipSuccess) {
       set_error("w8a8_gemm_kernel: cannot reserve %d bytes of LDS: %s", T::LDS, hipGetErrorString(e));
       return DC_EHIP;
     }
-    attr_set = true;
+    attr_set[dev].store(true, std::memory_order_release);
   }
   const unsigned ks = p.ksplit > 1 ? (unsigned)p.ksplit : 1u;
   hipLaunchKernelGGL((w8a8_gemm_kernel<T, OUT_DT, BIAS_DT>), dim3((unsigned)tiles, ks), dim3(T::NT), T::LDS, st, p);
@@ -704,17 +710,18 @@ static int launch_gemm_dma(GemmArgs p, hipStream_t st) {
   return launch_status("w8a8_gemm_dma_kernel");
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; concurrent first
+// calls store the same value).
 static int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (!n) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 // Tile shape by the fraction of the device the last round of tiles keeps busy,
@@ -907,7 +914,8 @@ extern "C" int dc_rescale(const int32_t* acc, int64_t lda, const float* sx, cons
   if (!acc || !sx || !sw || !out) return fail(DC_EINVAL, "dc_rescale: null pointer");
   if (lda < N || ldo < N) return fail(DC_EINVAL, "dc_rescale: leading dimension < N");
   if (bias_dtype != DC_NONE && !bias) return fail(DC_EINVAL, "dc_rescale: bias_dtype given without bias");
-  if (M * ((N + 3) / 4) > (int64_t)0x7fffffff * 256) return fail(DC_EINVAL, "dc_rescale: too large");
+  if (M > 0x7fffffff || N > 0x7fffffff || M * ((N + 3) / 4) > (int64_t)0x7fffffff * 256)
+    return fail(DC_EINVAL, "dc_rescale: size too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (out_dtype) {
     case DC_F16: return rescale_bias<DC_F16>(acc, lda, sx, sw, bias, bias_dtype, out, ldo, M, N, st);

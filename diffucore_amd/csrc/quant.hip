@@ -335,16 +335,23 @@ __global__ void __launch_bounds__(1024) quant_rows_lds_kernel(const void* __rest
 // it (src/diffucore/models/_int8.py:433-435: 0.5 h (1 + erf(h / sqrt 2)),
 // cast to the activation dtype; the tanh form is torch's
 // gelu(approximate="tanh"), 0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))),
-// which FLUX's MLPs use). Both are evaluated in forms without cancellation
-// in the negative tail and with the hardware exp2 / reciprocal (this pass is
-// VALU-bound, and the library erf / tanh cost about twice as much):
+// which FLUX's MLPs use). Both are evaluated in forms without the cancellation
+// the textbook forms have in the negative tail, with the hardware exp2 /
+// reciprocal (this pass is VALU-bound, and the library erf / tanh cost about
+// twice as much):
 //   tanh form: 0.5 x (1 + tanh u) = x / (1 + 2^(-2 u log2 e));
 //   erf form: 1 + erf(x / sqrt 2) = erfc(z) for x < 0, 2 - erfc(z) for x >= 0,
-//   z = |x| / sqrt 2, with erfc(z) = (a1 t + ... + a5 t^5) e^(-z^2),
-//   t = 1 / (1 + p z) (Abramowitz & Stegun 7.1.26, Hastings' approximation,
-//   |erf error| <= 1.5e-7).
-// Against float32 library GELU both stay within a few float32 ulp (absolute
-// ~1e-7 |x|), which the rounding to 16 bits hides but next to a boundary.
+//   z = |x| / sqrt 2, erfc by the Chebyshev-fitted form of Press et al.,
+//   Numerical Recipes (2nd ed., section 6.2, erfcc): t = 1 / (1 + z / 2),
+//   erfc(z) = t exp(-z^2 - 1.26551223 + t P(t)) with P of degree 9, whose
+//   relative error is below 1.2e-7 for every z >= 0.
+// Both keep a small relative error over the whole line. The reference's
+// cancelling forms do not: below x = -4 or so their float32 1 + erf / 1 + tanh
+// sits on the 2^-24 grid, and below about -5.5 they return -0. There the
+// values here are the accurate ones, so the 16-bit results can differ from the
+// reference's; those elements are below 1e-4 in magnitude (codes 0 unless a
+// whole row lies that far out). Elsewhere the two agree to a few float32 ulp,
+// which the rounding to 16 bits hides except next to a boundary.
 constexpr float LOG2E = 1.4426950408889634f;
 
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
@@ -355,12 +362,17 @@ __device__ __forceinline__ float gelu_tanh_f32(float x) {
 
 __device__ __forceinline__ float gelu_erf_f32(float x) {
   const float z = fabsf(x) * 0.7071067811865476f;
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
-  float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
-  poly = __builtin_fmaf(poly, t, 1.421413741f);
-  poly = __builtin_fmaf(poly, t, -0.284496736f);
-  poly = __builtin_fmaf(poly, t, 0.254829592f);
-  const float erfc = (poly * t) * __builtin_amdgcn_exp2f((z * z) * -LOG2E);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
+  float p = __builtin_fmaf(0.17087277f, t, -0.82215223f);
+  p = __builtin_fmaf(p, t, 1.48851587f);
+  p = __builtin_fmaf(p, t, -1.13520398f);
+  p = __builtin_fmaf(p, t, 0.27886807f);
+  p = __builtin_fmaf(p, t, -0.18628806f);
+  p = __builtin_fmaf(p, t, 0.09678418f);
+  p = __builtin_fmaf(p, t, 0.37409196f);
+  p = __builtin_fmaf(p, t, 1.00002368f);
+  p = __builtin_fmaf(p, t, -1.26551223f);
+  const float erfc = t * __builtin_amdgcn_exp2f(__builtin_fmaf(-z, z, p) * LOG2E);
   return (0.5f * x) * (x < 0.0f ? erfc : 2.0f - erfc);
 }
 
@@ -374,7 +386,7 @@ __device__ __forceinline__ float act_round(float x, int act) {
 // quantized exactly like quant_rows_lds_kernel. K1 and K are multiples of 256
 // (a 256-group never straddles the two sources), so each 8-lane group unit
 // reads one source.
-template <int DT, int S, bool ROT>
+template <int DT, int S, bool ROT, bool GEGLU>
 __global__ void __launch_bounds__(1024) quant_act_rows_kernel(const void* __restrict__ x1, int64_t ld1, int K1,
                                                               const void* __restrict__ x2, int64_t ld2, int K, int act,
                                                               int64_t M, int rpb, float inv_lr,
@@ -397,11 +409,25 @@ __global__ void __launch_bounds__(1024) quant_act_rows_kernel(const void* __rest
   int off[1][4];
   load_groups<DT, 1>(src, rowoff, second ? K - K1 : K1, second ? g - G1 : g, live ? (second ? G - G1 : G1) : 0, q8,
                      v, ok, off);
+  if constexpr (GEGLU) {
+    // x2 rows hold [value | gate], K - K1 wide each: y = round(value * round(gelu_erf(gate)))
+    float gt[1][4][8];
+    bool gok[1][4];
+    int goff[1][4];
+    load_groups<DT, 1>(src, rowoff + (second ? K - K1 : 0), second ? K - K1 : K1, second ? g - G1 : g,
+                       live && second ? G - G1 : 0, q8, gt, gok, goff);
+    if (second) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[0][j][e] = round_to<DT>(v[0][j][e] * act_round<DT>(gt[0][j][e], DC_ACT_GELU_ERF));
+    }
+  }
   if (second) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       off[0][j] += K1;
-      if (act != DC_ACT_NONE) {
+      if (!GEGLU && act != DC_ACT_NONE) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[0][j][e] = act_round<DT>(v[0][j][e], act);
       }
@@ -645,8 +671,13 @@ static int launch_act_s(const void* x1, int64_t ld1, int K1, const void* x2, int
   int rpb = 8 / (S / 8);
   while (rpb > 1 && rpb * lr > 1024) rpb /= 2;
   const int nt = (rpb * lr + 63) / 64 * 64;
-  hipLaunchKernelGGL((quant_act_rows_kernel<DT, S, ROT>), dim3((unsigned)((M + rpb - 1) / rpb)), dim3(nt), 0, st, x1,
-                     ld1, K1, x2, ld2, K, act, M, rpb, 1.0f / (float)lr, q, ldq, scale);
+  const dim3 grid((unsigned)((M + rpb - 1) / rpb));
+  if (act == DC_ACT_GEGLU)
+    hipLaunchKernelGGL((quant_act_rows_kernel<DT, S, ROT, true>), grid, dim3(nt), 0, st, x1, ld1, K1, x2, ld2, K, act,
+                       M, rpb, 1.0f / (float)lr, q, ldq, scale);
+  else
+    hipLaunchKernelGGL((quant_act_rows_kernel<DT, S, ROT, false>), grid, dim3(nt), 0, st, x1, ld1, K1, x2, ld2, K,
+                       act, M, rpb, 1.0f / (float)lr, q, ldq, scale);
   return launch_status("quant_act_rows_kernel");
 }
 
@@ -721,13 +752,15 @@ extern "C" int dc_act_quantize_rows(const void* x1, int64_t ld1, int64_t K1, con
                                     void* stream) {
   clear_error();
   const int64_t K = K1 + K2;
-  if (M < 0 || K1 < 0 || K2 < 0 || K <= 0 || ldq < K || (K1 && ld1 < K1) || (K2 && ld2 < K2))
+  const int64_t w2 = act == DC_ACT_GEGLU ? 2 * K2 : K2;   // x2 row width read
+  if (M < 0 || K1 < 0 || K2 < 0 || K <= 0 || ldq < K || (K1 && ld1 < K1) || (K2 && ld2 < w2))
     return fail(DC_EINVAL, "dc_act_quantize_rows: bad M/K1/K2/ld1/ld2/ldq");
   if (M == 0) return DC_OK;
   if (M > 0x7fffffff) return fail(DC_EINVAL, "dc_act_quantize_rows: M too large");
   if ((K1 && !x1) || (K2 && !x2) || !q || !scale) return fail(DC_EINVAL, "dc_act_quantize_rows: null pointer");
-  if (act != DC_ACT_NONE && act != DC_ACT_GELU_ERF && act != DC_ACT_GELU_TANH)
+  if (act != DC_ACT_NONE && act != DC_ACT_GELU_ERF && act != DC_ACT_GELU_TANH && act != DC_ACT_GEGLU)
     return fail(DC_EINVAL, "dc_act_quantize_rows: unknown act");
+  if (act == DC_ACT_GEGLU && K2 == 0) return fail(DC_EINVAL, "dc_act_quantize_rows: DC_ACT_GEGLU needs K2 > 0");
   if (group != 0 && group != 256) return fail(DC_EINVAL, "dc_act_quantize_rows: group must be 0 or 256");
   if (x_dtype != DC_F16 && x_dtype != DC_BF16) return fail(DC_EINVAL, "dc_act_quantize_rows: x_dtype must be DC_F16 or DC_BF16");
   if (K1 % 256 || K2 % 256 || K > 32768)

@@ -52,7 +52,7 @@ int dc_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
                      int8_t* q, int64_t ldq, float* scale, void* stream);
 
 /* Activations for dc_act_quantize_rows. */
-enum { DC_ACT_NONE = 0, DC_ACT_GELU_ERF = 1, DC_ACT_GELU_TANH = 2 };
+enum { DC_ACT_NONE = 0, DC_ACT_GELU_ERF = 1, DC_ACT_GELU_TANH = 2, DC_ACT_GEGLU = 3 };
 
 /*
  * dc_quantize_rows of the rows of concat(x1, act(x2)), in one pass:
@@ -68,6 +68,11 @@ enum { DC_ACT_NONE = 0, DC_ACT_GELU_ERF = 1, DC_ACT_GELU_TANH = 2 };
  * x1, its single-block linear2 input cat(attention, gelu_tanh(mlp))
  * (flux_dit.py:335), which the reference builds with torch ops before
  * quantizing.
+ * act = DC_ACT_GEGLU: x2 rows are [M, 2 K2] (row stride ld2 >= 2 K2), the
+ * value half then the gate half of a GEGLU projection, and the K2 columns fed
+ * to the quantizer are round(value * round(gelu_erf(gate))) (the SD1.5 / SDXL
+ * UNet's GEGLU, src/diffucore/models/unet.py:148-155: x * F.gelu(gate) on the
+ * two chunks of proj's output, each op rounded to x_dtype).
  */
 int dc_act_quantize_rows(const void* x1, int64_t ld1, int64_t K1, const void* x2, int64_t ld2, int64_t K2,
                          int act, int x_dtype, int64_t M, int group, int8_t* q, int64_t ldq, float* scale,

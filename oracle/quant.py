@@ -16,6 +16,8 @@ Follows reference ``src/diffucore/models/_int8.py``:
   ``_gelu_f16_rot_quant_kernel`` (``_int8.py:433-443``, ``_gelu_quantize``
   ``:348-358``); the tanh form is torch's ``gelu(approximate="tanh")`` that
   FLUX's MLPs use (``flux_dit.py:228-239, 335``).
+* ``geglu`` <- the UNet's ``GEGLU.forward`` (``unet.py:148-155``):
+  ``x * F.gelu(gate)`` on the two chunks of the projection output.
 """
 
 from __future__ import annotations
@@ -131,10 +133,22 @@ def gelu(x, approximate: str = "none", dtype: str = "bf16") -> np.ndarray:
     return round_to(y, dtype)
 
 
+def geglu(x2, dtype: str = "f16") -> np.ndarray:
+    """``x * gelu(gate)`` for ``x, gate = x2.chunk(2, -1)`` (``unet.py:148-155``):
+    the erf GELU of ``gate`` rounded to ``dtype`` (torch's half-precision
+    ``F.gelu``), then the product of two 16-bit values (exact in float32)
+    rounded to ``dtype`` once (torch's half-precision multiply)."""
+    x2 = np.asarray(x2, np.float32)
+    n = x2.shape[-1] // 2
+    x, gate = x2[..., :n], x2[..., n:]
+    return round_to((x * gelu(gate, "none", dtype)).astype(np.float32), dtype)
+
+
 def act_quantize(x2, group: int, approximate: str = "none", dtype: str = "bf16", prefix=None):
-    """``quantize_activation`` of the rows of ``cat(prefix, gelu(x2))``: what
-    the fused HIP kernel computes (prefix columns taken as they are)."""
-    h = gelu(x2, approximate, dtype)
+    """``quantize_activation`` of the rows of ``cat(prefix, act(x2))``: what
+    the fused HIP kernel computes (prefix columns taken as they are);
+    ``approximate`` is "none" / "tanh" (GELU forms) or "geglu"."""
+    h = geglu(x2, dtype) if approximate == "geglu" else gelu(x2, approximate, dtype)
     if prefix is not None:
         h = np.concatenate([np.asarray(prefix, np.float32), h], axis=-1)
     return quantize_activation(h, group)

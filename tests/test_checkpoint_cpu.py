@@ -90,6 +90,9 @@ def test_rejects_other_quantized_formats():
     assert D.int8_layers({"a.weight": torch.zeros(2, 2)}) == {}
     # convrot without a group size means the default group
     assert D.int8_layers({"a.comfy_quant": _tag(format="int8_tensorwise", convrot=True)}) == {"a": 256}
+    # a tag stored in a wider integer dtype holds the same byte values (the reference reads bytes(tag.tolist()))
+    wide = _tag(format="int8_tensorwise", convrot=True, convrot_groupsize=64).to(torch.int64)
+    assert D.int8_layers({"a.comfy_quant": wide}) == {"a": 64}
 
 
 def test_int8_embedding_rows_equal_the_dequantized_table():

@@ -148,3 +148,87 @@ def test_ln_mod_quantize_strided_modulation(gpu):
     sc1_s.copy_(sc1)
     q2, s2 = _int8.ln_mod_quantize(x, sc1_s, shift, L, 1e-6, 256)
     assert torch.equal(q, q2) and torch.equal(s, s2)
+
+
+# ---------------------------------------------------------------- GEGLU (SD1.5 / SDXL UNet feed-forward)
+
+@pytest.mark.parametrize("M,N,group,dtype", [
+    (8192, 5120, 256, torch.float16),     # SDXL 1024^2 level-1 blocks: GEGLU proj 640 -> 2 x 5120
+    (2048, 10240, 256, torch.float16),    # SDXL level-2 blocks: GEGLU proj 1280 -> 2 x 10240
+    (300, 1280, 0, torch.bfloat16),
+])
+def test_geglu_quantize_matches_unfused(gpu, M, N, group, dtype):
+    """The fused GEGLU middle (value * gelu(gate), each op rounded to the
+    dtype, then ConvRot + int8) against the reference's unfused torch ops on
+    the GPU and against the oracle, to the _agree bound."""
+    g = torch.Generator().manual_seed(M + N)
+    h = (torch.randn(M, 2 * N, generator=g) * 2).to(dtype).to(gpu)
+    q, s = _int8.act_quantize(h, group, "geglu")
+    assert q.shape == (M, N)
+    a, gate = h.chunk(2, dim=-1)
+    q_u, s_u = _int8.quantize_activation(a * F.gelu(gate), group)
+    _agree(q, s, q_u.cpu().numpy(), s_u.cpu().numpy())
+    q_o, s_o = OQ.act_quantize(np32(h), group, "geglu", DT[dtype])
+    _agree(q, s, q_o, s_o)
+    # geglu_quantize takes the fused path for these rows and gives the same
+    q2, s2 = _int8.geglu_quantize(h, group)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+
+
+def test_geglu_strided_projection_rows(gpu):
+    """The projection output as a column slice of a wider buffer (row stride >
+    2N), and a prefix: same codes as the contiguous copy."""
+    g = torch.Generator().manual_seed(31)
+    buf = torch.randn(129, 3 * 1024, generator=g).half().to(gpu)
+    h = buf[:, 512:512 + 2 * 1024]
+    pre = torch.randn(129, 256, generator=g).half().to(gpu)
+    q, s = _int8.act_quantize(h, 256, "geglu", prefix=pre)
+    q2, s2 = _int8.act_quantize(h.contiguous(), 256, "geglu", prefix=pre)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+    a, gate = h.chunk(2, dim=-1)
+    q_u, s_u = _int8.quantize_activation(torch.cat((pre, a * F.gelu(gate)), 1), 256)
+    _agree(q, s, q_u.cpu().numpy(), s_u.cpu().numpy())
+
+
+@pytest.mark.parametrize("act", ["gelu", "gelu_tanh"])
+def test_gelu_negative_tail(gpu, act):
+    """Rows that lie wholly in the negative tail (x in [-8, -3]), where the
+    reference's forms 0.5 x (1 + erf) / 0.5 x (1 + tanh) cancel: the kernel's
+    cancellation-free forms keep a small relative error, so its codes follow
+    the float64 GELU (rounded to the dtype, then quantized) within one step on
+    every element and exactly on at least 99% of them."""
+    from scipy.special import erfc
+    g = torch.Generator().manual_seed(41)
+    x = (torch.rand(64, 1024, generator=g) * -5 - 3).half().to(gpu)
+    q, s = _int8.act_quantize(x, 256, act)
+    xd = np32(x).astype(np.float64)
+    if act == "gelu":
+        y = 0.5 * xd * erfc(-xd / np.sqrt(2))          # 1 + erf(z) = erfc(-z), no cancellation
+    else:
+        u = np.sqrt(2 / np.pi) * (xd + 0.044715 * xd ** 3)
+        y = xd / (1 + np.exp(-2 * u))
+    q_ref, s_ref = OQ.quantize_activation(y.astype(np.float32).astype(np.float16).astype(np.float32), 256)
+    qn, sn = q.cpu().numpy().astype(np.int32), s.cpu().numpy()
+    assert np.all(np.abs(sn - s_ref) <= s_ref * 2 ** -8)
+    d = np.abs(qn - q_ref.astype(np.int32))
+    assert d.max() <= 1 and (d == 0).mean() >= 0.99, (d == 0).mean()
+
+
+@pytest.mark.parametrize("dim,bias", [(640, True), (1280, False)])
+def test_int8_geglu_ff_matches_eager(gpu, dim, bias):
+    """int8_geglu_ff (fused middle) against the same two Int8Linear layers run
+    eagerly, out(x * gelu(gate)), and against the float feed-forward."""
+    torch.manual_seed(dim)
+    inner = 4 * dim
+    proj = nn.Linear(dim, 2 * inner, bias=bias).to(gpu).half()
+    out = nn.Linear(inner, dim, bias=bias).to(gpu).half()
+    lp, lo = _int8.Int8Linear.from_linear(proj, 256), _int8.Int8Linear.from_linear(out, 256)
+    x = torch.randn(2, 1024, dim, device=gpu, dtype=torch.float16)
+    y = _int8.int8_geglu_ff(x, lp, lo)
+    a, gate = lp(x).chunk(2, dim=-1)
+    y_eager = lo(a * F.gelu(gate))
+    assert y.shape == y_eager.shape == (2, 1024, dim) and y.dtype == torch.float16
+    assert rel_l2(np32(y), np32(y_eager)) < 2e-3
+    af, gf = proj(x).chunk(2, dim=-1)
+    y_float = out(af * F.gelu(gf))
+    assert rel_l2(np32(y), np32(y_float)) < 3e-2 and cosine(np32(y), np32(y_float)) > 0.999

@@ -1,0 +1,88 @@
+"""The full synthetic FLUX.1-schnell denoise step on the
+GPU: the DiT of ``flux_step.py`` (a restatement of the reference's
+``flux_dit.py:254-447``) at full width and full token count (hidden 3072,
+24 heads, 4096 image + 512 text tokens) with reduced depth (2 double + 2
+single blocks), and the schnell Euler loop (``pipelines/_flux.py:229-236``).
+
+Two comparisons, on the same seeded weights and inputs:
+  (i)  INT8 attention + W8A8 linears + the fused glue passes against the
+       reference's bf16 eager step (bf16 SDPA, bf16 linears), on one forward
+       and on the 4-step final latent;
+  (ii) the INT8 step with the fused glue passes against the INT8 step with
+       the reference's eager glue (LayerNorm-modulate, QK RMSNorm + rotary,
+       GELU, concatenation as torch ops): the same int8 weights, so only the
+       glue's rounding differs.
+The bounds are stated in each test; the measured values are printed.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import flux_step as FS
+from diffucore_amd import quantize_linears, set_attention_backend, set_fused_glue
+from tests._util import cosine, np32, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def flux(gpu):
+    shape = FS.FluxShape(depth=2, depth_single=2)
+    model = FS.build(shape, gpu, torch.bfloat16, seed=0)
+    x0, txt, y, pe = FS.inputs(shape, gpu, torch.bfloat16, seed=1)
+    sigmas = FS.schnell_sigmas(4, gpu)
+    t = sigmas[:1].to(torch.bfloat16)
+    with torch.no_grad():
+        v_bf16 = model(x0, txt, t, y, pe)
+        lat_bf16 = FS.denoise(model, x0, txt, y, pe, sigmas)
+    quantize_linears(model, FS.block_linear_names(model), gpu, 256)
+    set_attention_backend(model, "int8_turing")
+    yield dict(model=model, x0=x0, txt=txt, y=y, pe=pe, sigmas=sigmas, t=t, v_bf16=v_bf16, lat_bf16=lat_bf16)
+    del model
+    torch.cuda.empty_cache()
+
+
+def _run(f, fused: bool):
+    m = f["model"]
+    set_fused_glue(m, fused)
+    with torch.no_grad():
+        v = m(f["x0"], f["txt"], f["t"], f["y"], f["pe"])
+        lat = FS.denoise(m, f["x0"], f["txt"], f["y"], f["pe"], f["sigmas"])
+    torch.cuda.synchronize()
+    return v, lat
+
+
+def test_int8_step_against_bf16_eager(flux):
+    """(i) One forward: rel L2 < 5e-2 and cosine > 0.998 on the velocity;
+    4-step final latent: rel L2 < 2e-2 and cosine > 0.9998 (the full 57-block
+    model measures rel L2 0.025, cos 0.9997 on its latent)."""
+    v, lat = _run(flux, fused=True)
+    assert v.shape == flux["v_bf16"].shape and v.dtype == torch.bfloat16
+    assert torch.isfinite(v).all() and torch.isfinite(lat).all()
+    rv, cv = rel_l2(np32(v), np32(flux["v_bf16"])), cosine(np32(v), np32(flux["v_bf16"]))
+    rl, cl = rel_l2(np32(lat), np32(flux["lat_bf16"])), cosine(np32(lat), np32(flux["lat_bf16"]))
+    print(f"\n[flux step] velocity rel_l2 {rv:.4g} cos {cv:.6f}; latent rel_l2 {rl:.4g} cos {cl:.6f}")
+    assert rv < 5e-2 and cv > 0.998
+    assert rl < 2e-2 and cl > 0.9998
+
+
+def test_fused_glue_against_eager_glue(flux):
+    """(ii) Same int8 weights, fused against eager glue: rel L2 < 1.5e-2 and
+    cosine > 0.9999 on the velocity and on the latent."""
+    v_f, lat_f = _run(flux, fused=True)
+    v_e, lat_e = _run(flux, fused=False)
+    rv, cv = rel_l2(np32(v_f), np32(v_e)), cosine(np32(v_f), np32(v_e))
+    rl, cl = rel_l2(np32(lat_f), np32(lat_e)), cosine(np32(lat_f), np32(lat_e))
+    print(f"\n[flux step] fused vs eager glue: velocity rel_l2 {rv:.4g} cos {cv:.6f}; latent rel_l2 {rl:.4g} "
+          f"cos {cl:.6f}")
+    assert rv < 1.5e-2 and cv > 0.9999
+    assert rl < 1.5e-2 and cl > 0.9999
+
+
+def test_int8_step_is_deterministic(flux):
+    """Two runs of the INT8 step on the same inputs give the same bits."""
+    v1, lat1 = _run(flux, fused=True)
+    v2, lat2 = _run(flux, fused=True)
+    assert torch.equal(v1, v2) and torch.equal(lat1, lat2)

@@ -241,6 +241,168 @@ def test_q_quantize_properties():
     assert qs[0, 1, 7] == 0 and not q8[0, 1, 7].any()
 
 
+# ---------------------------------------------------------------- attention quantizer codes, exact
+
+def _rne_int(x: Fraction) -> int:
+    """Nearest integer to an exact rational, ties to even."""
+    f = x.numerator // x.denominator
+    rem = x - f
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and f % 2):
+        f += 1
+    return f
+
+
+def _exact_attn_codes(rows) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's attention quantizer (int8_attn_sm80.cu:75-85, 369-378)
+    in exact rational arithmetic: per row, inv = RN(127 / amax) (a float32
+    division), code = rint_even(RN(x * inv)) (a float32 multiply, then
+    __float2int_rn; no clamp), scale = RN(amax / 127); a zero row has codes 0
+    and scale 0."""
+    rows = _f32(rows)
+    codes = np.zeros(rows.shape, np.int64)
+    scales = np.zeros(rows.shape[0], np.float32)
+    for i, row in enumerate(rows):
+        amax = max(abs(Fraction(float(x))) for x in row)
+        if amax == 0:
+            continue
+        inv = Fraction(float(_round_exact_to_f32(Fraction(127) / amax)))
+        scales[i] = _round_exact_to_f32(amax / 127)
+        for j, x in enumerate(row):
+            codes[i, j] = _rne_int(Fraction(float(_round_exact_to_f32(Fraction(float(x)) * inv))))
+    return codes, scales
+
+
+def _boundary_rows(rng, n: int, d: int, dtype=torch.bfloat16) -> np.ndarray:
+    """Rows whose codes separate the plausible roundings of the quantizer:
+    each holds its absmax a and a/2 (the code-63/64 boundary, where x * RN(127/a)
+    and x / RN(a/127) round differently for some a), +-a/2 and half-integer
+    multiples of a/127 (exact ties when a = 127), and random fill."""
+    rows = torch.randn(n, d, generator=torch.Generator().manual_seed(int(rng.integers(1 << 30)))).to(dtype).float()
+    amax = rows.abs().amax(1)
+    rows[:, 0] = amax
+    rows[:, 1] = amax / 2
+    rows[:, 2] = -amax / 2
+    rows[: n // 4, 0] = 127.0             # a = 127: inv = 1 exactly, so x = k + 1/2 is a tie
+    for j, t in enumerate((0.5, 1.5, 2.5, -2.5, 126.5, -3.5)):
+        rows[: n // 4, 3 + j] = t
+    rows[n - 1] = 0.0                     # zero row
+    return rows.to(dtype).float().numpy()
+
+
+def _attn_amaxes_with_boundary_cases(dtype=torch.bfloat16) -> list:
+    """absmax values a (representable in ``dtype``) for which the divide form
+    rint(RN(a/2 / RN(a/127))) differs from the multiply form rint(RN(a/2 * RN(127/a)))."""
+    b = np.arange(0x3c00, 0x4100, dtype=np.uint32) << 16        # bf16 values in [2^-7, 8)
+    a = b.view(np.float32)
+    a = torch.tensor(a).to(dtype).float().numpy()
+    half = (a / np.float32(2)).astype(np.float32)
+    mul = np.rint((half * (np.float32(127) / a)).astype(np.float32))
+    div = np.rint((half / (a / np.float32(127))).astype(np.float32))
+    return sorted(set(a[mul != div].tolist()))
+
+
+def _q_codes_pinned(q_quantize) -> bool:
+    rows = _boundary_rows(np.random.default_rng(5), 48, 64)
+    amaxes = _attn_amaxes_with_boundary_cases()
+    for i, a in enumerate(amaxes[:16]):   # rows whose a/2 sits on a multiply/divide disagreement
+        rows[12 + i, :] = np.clip(rows[12 + i, :], -a, a)
+        rows[12 + i, 0], rows[12 + i, 1], rows[12 + i, 2] = a, a / 2, -a / 2
+    exact_codes, exact_scales = _exact_attn_codes(rows)
+    q8, qs = q_quantize(rows.reshape(1, 48, 1, 64))
+    return (np.array_equal(q8[0, 0].astype(np.int64), exact_codes)
+            and np.array_equal(qs[0, 0], exact_scales))
+
+
+def _k_codes_pinned(k_quantize) -> bool:
+    """K blocks of 64 keys whose column sums are exactly zero (key r + 16 is
+    the negation of key r inside each group of 32, so every float32 partial sum
+    returns to +-0), making the smoothed keys equal the keys; each block's
+    codes then follow the exact quantizer over the block's 64 x D values."""
+    D, L = 16, 192
+    rng = np.random.default_rng(6)
+    base = _boundary_rows(rng, L // 2, D)
+    amaxes = _attn_amaxes_with_boundary_cases()
+    k = np.zeros((L, D), np.float32)
+    for g in range(L // 32):
+        half = base[16 * (g % 3):16 * (g % 3) + 16].copy()   # g = 4: rows with a = 127 and exact ties
+        if g < 3:                          # a block-wide absmax a with a/2 present
+            a = amaxes[4 * g]
+            half = np.clip(half, -a, a)
+            half[0, 0], half[1, 0] = a, a / 2
+        k[32 * g:32 * g + 16] = half
+        k[32 * g + 16:32 * g + 32] = -half
+    assert not OA.k_colsum(k.reshape(1, L, 1, D)).any()
+    ki, ks = k_quantize(k.reshape(1, L, 1, D))
+    blocks = k.reshape(L // 64, 64 * D)
+    exact_codes, exact_scales = _exact_attn_codes(blocks)
+    return (np.array_equal(ki[0, 0].reshape(L // 64, 64 * D).astype(np.int64), exact_codes)
+            and np.array_equal(ks[0, 0], exact_scales))
+
+
+def _divide_form_q(q):
+    """Planted mistake: the linear quantizer's division instead of the multiply."""
+    q = _f32(q).transpose(0, 2, 1, 3)
+    amax = np.abs(q).max(axis=-1)
+    s = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q8 = np.where(s[..., None] > 0, np.rint((q / s[..., None]).astype(np.float32)), 0).astype(np.int8)
+    return q8, s
+
+
+def _clamped_floor_q(q):
+    """Planted mistake: the linear quantizer whole (scale floored at 1e-30, clamp)."""
+    q = _f32(q).transpose(0, 2, 1, 3)
+    s = np.maximum(np.abs(q).max(axis=-1) / np.float32(127.0), np.float32(1e-30)).astype(np.float32)
+    return np.clip(np.rint((q / s[..., None]).astype(np.float32)), -128, 127).astype(np.int8), s
+
+
+def _half_away_q(q):
+    """Planted mistake: round half away from zero."""
+    q = _f32(q).transpose(0, 2, 1, 3)
+    amax = np.abs(q).max(axis=-1)
+    with np.errstate(divide="ignore"):
+        inv = np.where(amax > 0, np.float32(127.0) / amax, np.float32(0.0)).astype(np.float32)
+    p = (q * inv[..., None]).astype(np.float32)
+    return (np.sign(p) * np.floor(np.abs(p) + 0.5)).astype(np.int8), (amax / np.float32(127.0)).astype(np.float32)
+
+
+def test_boundary_inputs_separate_multiply_and_divide_forms():
+    amaxes = _attn_amaxes_with_boundary_cases()
+    assert len(amaxes) >= 16
+    codes_mul = _exact_attn_codes(np.array([[a, a / 2] for a in amaxes[:16]], np.float32))[0][:, 1]
+    assert set(codes_mul.tolist()) <= {63, 64} and len(set(codes_mul.tolist())) == 2
+
+
+def test_q_quantize_codes_exact():
+    assert _q_codes_pinned(OA.q_quantize)
+
+
+def test_k_quantize_codes_exact():
+    assert _k_codes_pinned(OA.k_quantize)
+
+
+@pytest.mark.parametrize("mutant", [_divide_form_q, _clamped_floor_q, _half_away_q])
+def test_q_code_pin_catches_planted_mistakes(mutant):
+    assert not _q_codes_pinned(mutant)
+
+
+@pytest.mark.parametrize("mutant", [_divide_form_q, _clamped_floor_q, _half_away_q])
+def test_k_code_pin_catches_planted_mistakes(mutant, monkeypatch):
+    # the same mistakes in the K quantizer's per-block code step
+    def k_mut(k, ksum=None):
+        k = _f32(k)
+        B, L, H, D = k.shape
+        ks_ = OA.k_colsum(k) if ksum is None else ksum
+        val = OA.k_smooth(k, ks_)                                        # [B, H, L, D]
+        nblk = -(-L // 64)
+        pad = np.zeros((B, H, nblk * 64, D), np.float32)
+        pad[:, :, :L] = val
+        blocks = pad.reshape(B * H * nblk, 1, 1, 64 * D).transpose(0, 2, 1, 3)   # rows = blocks
+        c, s = mutant(blocks)
+        return c.reshape(B, H, nblk * 64, D), s.reshape(B, H, nblk)
+    assert not _k_codes_pinned(k_mut)
+
+
 # ---------------------------------------------------------------- attention output
 
 def _sdpa(q, k, v):
@@ -342,6 +504,59 @@ def test_act_quantize_oracle_is_quantize_of_gelu():
     pre = g.standard_normal((5, 256)).astype(np.float32)
     q, s = OQ.act_quantize(x, 256, "tanh", "bf16", prefix=pre)
     q2, s2 = OQ.quantize_activation(np.concatenate([pre, OQ.gelu(x, "tanh", "bf16")], 1), 256)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+
+def _geglu_torch(x2: np.ndarray, tdt) -> np.ndarray:
+    """The reference statement (unet.py:148-155), x * F.gelu(gate) on the two
+    chunks in the 16-bit dtype, as torch runs it on the GPU: the GELU in
+    float32 rounded to the dtype (torch's opmath for half types; its CPU half
+    kernel uses a coarser erf in the tail), then the product rounded once."""
+    t = torch.from_numpy(x2).to(tdt)
+    a, gate = t.chunk(2, dim=-1)
+    return (a * F.gelu(gate.float()).to(tdt)).float().numpy()
+
+
+@pytest.mark.parametrize("dt,tdt", [("f16", torch.float16), ("bf16", torch.bfloat16)])
+def test_geglu_oracle_against_torch_statement(dt, tdt):
+    """The GEGLU oracle equals torch's ops except next to a rounding boundary
+    of the GELU. For gates below about -2.5 both compute 1 + erf next to
+    cancellation, where one ulp of the float32 erf moves the GELU by up to
+    |gate| 2^-24 (the same allowance as the GELU pin): those products agree to
+    |x| 1e-5."""
+    g = torch.Generator().manual_seed(21)
+    x2 = (torch.randn(64, 1024, generator=g) * 2).to(tdt).float().numpy()
+    o = OQ.geglu(x2, dt)
+    r = _geglu_torch(x2, tdt)
+    assert o.shape == (64, 512)
+    x, gate = x2[:, :512], x2[:, 512:]
+    core = gate >= -2.5
+    assert (o[core] == r[core]).mean() > 0.999, (o[core] == r[core]).mean()
+    assert np.all(np.abs(o - r) <= np.maximum(np.abs(r) * 2 ** -6, np.abs(x) * 1e-5))
+
+
+def test_geglu_oracle_closed_forms_and_rounding_order():
+    """gate = 0 gives 0; gate >= 8 has gelu(gate) = gate, so the result is
+    round(x * gate); a planted form that skips the GELU's own rounding (one
+    rounding of x * gelu(gate)) differs from torch's two-rounding statement."""
+    x = np.array([[1.5, -2.25, 3.0, 0.7, 0.0, 9.0, 12.0, 1.0]], np.float32)
+    o = OQ.geglu(x, "f16")
+    assert o[0, 0] == 0 and o[0, 1] == np.float32(np.float16(-2.25 * 9.0))
+    assert o[0, 2] == np.float32(np.float16(3.0 * 12.0))
+    g = torch.Generator().manual_seed(22)
+    x2 = (torch.randn(256, 1024, generator=g) * 2).half().float().numpy()
+    one_rounding = OF.round_to((x2[:, :512] * OQ.gelu(x2[:, 512:], "none", "f32")).astype(np.float32), "f16")
+    r = _geglu_torch(x2, torch.float16)
+    assert (one_rounding != r).mean() > 10 * (OQ.geglu(x2, "f16") != r).mean() + 1e-4
+
+
+def test_act_quantize_oracle_geglu_is_quantize_of_geglu():
+    g = np.random.default_rng(23)
+    x2 = g.standard_normal((6, 1024)).astype(np.float32)
+    pre = g.standard_normal((6, 256)).astype(np.float32)
+    q, s = OQ.act_quantize(x2, 256, "geglu", "f16", prefix=pre)
+    q2, s2 = OQ.quantize_activation(np.concatenate([pre, OQ.geglu(x2, "f16")], 1), 256)
     assert np.array_equal(q, q2) and np.array_equal(s, s2)
 
 

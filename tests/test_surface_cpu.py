@@ -57,6 +57,25 @@ def test_null_keys_equal_padded():
     assert torch.equal(D.attention_blhd(q, k, v, null_keys=5), D.attention_blhd(q, F.pad(k, pad), F.pad(v, pad)))
 
 
+def test_int8_guard_needs_paired_shapes():
+    """The per-call guard sends calls whose operands do not pair up (batch,
+    heads, key/value lengths) or have an empty sequence to SDPA instead of the
+    kernel's shape error."""
+    ok = _attention._blhd_compatible
+    z = torch.zeros
+    assert ok(z(2, 64, 4, 64), z(2, 77, 4, 64), z(2, 77, 4, 64))
+    assert not ok(z(2, 64, 4, 64), z(1, 77, 4, 64), z(1, 77, 4, 64))      # batch
+    assert not ok(z(2, 64, 4, 64), z(2, 77, 2, 64), z(2, 77, 2, 64))      # heads
+    assert not ok(z(2, 64, 4, 64), z(2, 77, 4, 64), z(2, 76, 4, 64))      # k / v lengths
+    assert not ok(z(2, 0, 4, 64), z(2, 77, 4, 64), z(2, 77, 4, 64))       # no queries
+    assert not ok(z(2, 64, 4, 64), z(2, 0, 4, 64), z(2, 0, 4, 64))        # no keys
+    assert not ok(z(64, 4, 64), z(2, 77, 4, 64), z(2, 77, 4, 64))         # not 4-d
+    # SDPA takes an empty key set on the int8 backend's fallback path
+    q = torch.randn(1, 5, 2, 64)
+    out = D.attention_blhd(q, torch.zeros(1, 0, 2, 64), torch.zeros(1, 0, 2, 64), "int8_turing")
+    assert out.shape == (1, 5, 128)
+
+
 def test_policy_resolution():
     assert D.resolve_attention_backend(_CPU) == "sdpa"
     auto = D.DevicePolicy(device=torch.device("cpu"), compute_dtype=torch.float32, attention="auto")
@@ -229,6 +248,14 @@ def test_argument_checks_fail_before_any_launch():
     assert qk(_lib.BF16, 1, 64, wdt=_lib.F16) == 1 and b"weight_dtype" in so.dc_last_error()
     assert qk(_lib.BF16, 1, 64, flags=4) == 1 and b"flags" in so.dc_last_error()
     assert qk(_lib.BF16, 1, 64, eps=-1.0) == 1 and b"eps" in so.dc_last_error()
+    # dc_rescale: M or N beyond int range is rejected (the kernel indexes rows in int)
+    assert so.dc_rescale(16, 4, 16, 16, None, -1, 16, _lib.BF16, 4, (1 << 31) + 5, 4, None) == 1
+    assert b"too large" in so.dc_last_error()
+    # dc_act_quantize_rows, GEGLU: x2 rows must hold 2 * K2 values
+    assert so.dc_act_quantize_rows(None, 0, 0, 16, 256, 256, 3, _lib.F16, 4, 256, 16, 256, 16, None) == 1
+    assert b"ld2" in so.dc_last_error()
+    assert so.dc_act_quantize_rows(None, 0, 0, 16, 512, 256, 4, _lib.F16, 4, 256, 16, 256, 16, None) == 1
+    assert b"unknown act" in so.dc_last_error()
 
 
 def test_bench_refuses_more_than_one_gpu():
