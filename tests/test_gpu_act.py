@@ -222,7 +222,9 @@ def test_int8_geglu_ff_matches_eager(gpu, dim, bias):
     inner = 4 * dim
     proj = nn.Linear(dim, 2 * inner, bias=bias).to(gpu).half()
     out = nn.Linear(inner, dim, bias=bias).to(gpu).half()
-    lp, lo = _int8.Int8Linear.from_linear(proj, 256), _int8.Int8Linear.from_linear(out, 256)
+    # ConvRot group 256 where the input width allows it, else none (SDXL's 640-wide blocks)
+    lp = _int8.Int8Linear.from_linear(proj, 256 if dim % 256 == 0 else 0)
+    lo = _int8.Int8Linear.from_linear(out, 256)
     x = torch.randn(2, 1024, dim, device=gpu, dtype=torch.float16)
     y = _int8.int8_geglu_ff(x, lp, lo)
     a, gate = lp(x).chunk(2, dim=-1)
