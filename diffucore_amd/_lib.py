@@ -16,7 +16,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libdiffucore_amd.so"
 
 F16, BF16, F32, I32, NONE = 0, 1, 2, 3, -1
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _DTYPE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int32: I32}
 
@@ -42,6 +42,9 @@ _SIGS = {
     "dc_int8_attn_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                               ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
                               ctypes.POINTER(_I64), ctypes.c_float, _P, ctypes.c_size_t, _P]),
+    "dc_int8_attn_fwd_noalloc": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                      ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
+                                      ctypes.POINTER(_I64), ctypes.c_float, _P]),
     "dc_int8_attn_quantize_q": (_I, [_P, _I, _I, _I, _I, _I, ctypes.POINTER(_I64), _P, _P, _P]),
 }
 SYMBOLS = tuple(_SIGS)

@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 namespace dc {
 
@@ -879,10 +880,6 @@ static int check_args(const void* q, int dtype, int B, int H, int Lq, int D, con
   return DC_OK;
 }
 
-}  // namespace dc
-
-using namespace dc;
-
 extern "C" size_t dc_int8_attn_workspace_bytes(int B, int H, int Lq, int Lk, int D) {
   if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D <= 0 || D > 128) return 0;
   // room for the larger of the two dtypes' plans
@@ -908,26 +905,34 @@ extern "C" int dc_int8_attn_plan(int dtype, int B, int H, int Lq, int Lk, int D,
   return DC_OK;
 }
 
-extern "C" int dc_int8_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Lq,
-                                int Lk, int D, const int64_t q_strides[3], const int64_t k_strides[3],
-                                const int64_t v_strides[3], const int64_t o_strides[3], float sm_scale,
-                                void* workspace, size_t ws_bytes, void* stream) {
-  clear_error();
+// Shared body of dc_int8_attn_fwd and dc_int8_attn_fwd_noalloc: checks,
+// workspace carve-up and launches. `who` names the entry point in messages.
+static int attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Lq, int Lk,
+                    int D, const int64_t q_strides[3], const int64_t k_strides[3], const int64_t v_strides[3],
+                    const int64_t o_strides[3], float sm_scale, void* workspace, size_t ws_bytes, void* stream,
+                    const char* who) {
   AttnArgs a{};
   if (int e = check_args(q, dtype, B, H, Lq, D, q_strides, a)) return e;
-  if (Lk <= 0) return fail(DC_EINVAL, "dc_int8_attn_fwd: empty attention input");
-  if (!k || !v || !o || !k_strides || !v_strides || !o_strides) return fail(DC_EINVAL, "dc_int8_attn_fwd: null pointer");
-  if (!aligned16(k) || !aligned16(v) || !aligned16(o))
-    return fail(DC_EUNSUPPORTED, "dc_int8_attn_fwd: q, k, v, o must be 16-byte aligned");
+  if (Lk <= 0) { set_error("%s: empty attention input", who); return DC_EINVAL; }
+  if (!k || !v || !o || !k_strides || !v_strides || !o_strides) { set_error("%s: null pointer", who); return DC_EINVAL; }
+  if (!aligned16(k) || !aligned16(v) || !aligned16(o)) {
+    set_error("%s: q, k, v, o must be 16-byte aligned", who);
+    return DC_EUNSUPPORTED;
+  }
   for (int i = 0; i < 3; ++i)
     if (k_strides[i] % 8 || v_strides[i] % 8 || o_strides[i] % 8 || k_strides[i] < 0 || v_strides[i] < 0 ||
-        o_strides[i] < 0)
-      return fail(DC_EUNSUPPORTED, "dc_int8_attn_fwd: (B, L, H) strides must be non-negative multiples of 8");
-  if ((int64_t)Lk + WIN > 0x7fffffff) return fail(DC_EINVAL, "dc_int8_attn_fwd: problem too large");
+        o_strides[i] < 0) {
+      set_error("%s: (B, L, H) strides must be non-negative multiples of 8", who);
+      return DC_EUNSUPPORTED;
+    }
+  if ((int64_t)Lk + WIN > 0x7fffffff) { set_error("%s: problem too large", who); return DC_EINVAL; }
   const AttnPlan pl = D <= 64 ? attn_plan_dp<64>(dtype, B, H, Lq, Lk) : attn_plan_dp<128>(dtype, B, H, Lq, Lk);
   const WsLayout w = ws_layout(B, H, Lk, D, pl.sk_blocks);
-  if (!workspace || ws_bytes < w.total) return fail(DC_EWORKSPACE, "dc_int8_attn_fwd: workspace too small");
-  if (!aligned16(workspace)) return fail(DC_EWORKSPACE, "dc_int8_attn_fwd: workspace must be 16-byte aligned");
+  if (!workspace || ws_bytes < w.total) {
+    set_error("%s: workspace too small (%zu bytes, this call needs %zu)", who, ws_bytes, w.total);
+    return DC_EWORKSPACE;
+  }
+  if (!aligned16(workspace)) { set_error("%s: workspace must be 16-byte aligned", who); return DC_EWORKSPACE; }
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   a.k = k; a.v = v; a.o = o;
   a.k8 = reinterpret_cast<int8_t*>(ws + w.k8);
@@ -948,6 +953,78 @@ extern "C" int dc_int8_attn_fwd(const void* q, const void* k, const void* v, voi
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == DC_BF16) return D <= 64 ? launch_attn<DC_BF16, 64>(a, st) : launch_attn<DC_BF16, 128>(a, st);
   return D <= 64 ? launch_attn<DC_F16, 64>(a, st) : launch_attn<DC_F16, 128>(a, st);
+}
+
+// ---------------------------------------------------------------- no-allocation entry point
+
+// Scratch of dc_int8_attn_fwd_noalloc: a file-scope device array (each GPU
+// the library runs on holds its own copy, of DC_ATTN_NOALLOC_MAX_BYTES, until
+// the process ends). Its name is a host-side stand-in, not a device address:
+// host code uses only the per-device pointer hipGetSymbolAddress returns,
+// looked up once per device with that device current.
+static __device__ __align__(256) uint8_t scratch[DC_ATTN_NOALLOC_MAX_BYTES];
+
+constexpr int SCRATCH_DEVICES = 64;
+static std::once_flag scratch_once[SCRATCH_DEVICES];
+static void* scratch_ptr[SCRATCH_DEVICES];
+static hipError_t scratch_err[SCRATCH_DEVICES];
+
+// This device's copy of `scratch` (looked up on the first call per device).
+static int device_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_DEVICES)
+    return fail(DC_EHIP, "dc_int8_attn_fwd_noalloc: no current HIP device");
+  std::call_once(scratch_once[dev], [dev] {
+    void* p = nullptr;
+    scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    scratch_ptr[dev] = p;
+  });
+  if (scratch_err[dev] != hipSuccess || !scratch_ptr[dev]) {
+    set_error("dc_int8_attn_fwd_noalloc: hipGetSymbolAddress of the scratch array failed: %s",
+              hipGetErrorString(scratch_err[dev]));
+    return DC_EHIP;
+  }
+  *out = scratch_ptr[dev];
+  return DC_OK;
+}
+
+}  // namespace dc
+
+using namespace dc;
+
+extern "C" int dc_int8_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Lq,
+                                int Lk, int D, const int64_t q_strides[3], const int64_t k_strides[3],
+                                const int64_t v_strides[3], const int64_t o_strides[3], float sm_scale,
+                                void* workspace, size_t ws_bytes, void* stream) {
+  clear_error();
+  return attn_fwd(q, k, v, o, dtype, B, H, Lq, Lk, D, q_strides, k_strides, v_strides, o_strides, sm_scale, workspace,
+                  ws_bytes, stream, "dc_int8_attn_fwd");
+}
+
+extern "C" int dc_int8_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
+                                        int Lq, int Lk, int D, const int64_t q_strides[3],
+                                        const int64_t k_strides[3], const int64_t v_strides[3],
+                                        const int64_t o_strides[3], float sm_scale, void* stream) {
+  clear_error();
+  if (dtype != DC_F16 && dtype != DC_BF16)
+    return fail(DC_EINVAL, "dc_int8_attn_fwd_noalloc: dtype must be DC_F16 or DC_BF16");
+  if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0) return fail(DC_EINVAL, "dc_int8_attn_fwd_noalloc: empty attention input");
+  if (D <= 0 || D > 128 || D % 8)
+    return fail(DC_EUNSUPPORTED, "dc_int8_attn_fwd_noalloc: head dim must be a multiple of 8, <= 128");
+  if ((int64_t)B * H * ((Lq + BQ - 1) / BQ) > 0x7fffffff || (int64_t)Lq + BQ > 0x7fffffff ||
+      (int64_t)Lk + WIN > 0x7fffffff)
+    return fail(DC_EINVAL, "dc_int8_attn_fwd_noalloc: problem too large");
+  const AttnPlan pl = D <= 64 ? attn_plan_dp<64>(dtype, B, H, Lq, Lk) : attn_plan_dp<128>(dtype, B, H, Lq, Lk);
+  const size_t need = ws_layout(B, H, Lk, D, pl.sk_blocks).total;
+  if (need > DC_ATTN_NOALLOC_MAX_BYTES) {
+    set_error("dc_int8_attn_fwd_noalloc: this call needs %zu bytes of scratch, more than the %zu it holds; use "
+              "dc_int8_attn_fwd with a workspace", need, (size_t)DC_ATTN_NOALLOC_MAX_BYTES);
+    return DC_EWORKSPACE;
+  }
+  void* ws = nullptr;
+  if (int e = device_scratch(&ws)) return e;
+  return attn_fwd(q, k, v, o, dtype, B, H, Lq, Lk, D, q_strides, k_strides, v_strides, o_strides, sm_scale, ws,
+                  DC_ATTN_NOALLOC_MAX_BYTES, stream, "dc_int8_attn_fwd_noalloc");
 }
 
 extern "C" int dc_int8_attn_quantize_q(const void* q, int dtype, int B, int H, int Lq, int D,

@@ -233,6 +233,29 @@ int dc_int8_attn_fwd(const void* q, const void* k, const void* v, void* o, int d
                      const int64_t o_strides[3], float sm_scale, void* workspace,
                      size_t ws_bytes, void* stream);
 
+/* Scratch bytes dc_int8_attn_fwd_noalloc holds on each GPU it runs on (64 MiB). */
+#define DC_ATTN_NOALLOC_MAX_BYTES (64u << 20)
+
+/*
+ * dc_int8_attn_fwd without a workspace argument: the same kernels and work
+ * split, with the workspace taken from a scratch array the library keeps in
+ * device memory (DC_ATTN_NOALLOC_MAX_BYTES per GPU, held until the process
+ * ends). No counterpart in the reference (whose fwd allocates its scratch
+ * through torch, int8_attn_sm80.cu:469-476): it is for callers that cannot
+ * allocate - code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. It calls no hipMalloc / hipFree. A call whose
+ * workspace (dc_int8_attn_workspace_bytes) would exceed the scratch returns
+ * DC_EWORKSPACE with a message (FLUX 1024^2 attention needs 14.7 MB). Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (two streams, two threads) race and must be ordered by the caller; calls in
+ * one stream are ordered already. Nothing in the scratch needs to start at
+ * zero (every byte a call reads, it wrote first).
+ */
+int dc_int8_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                             int H, int Lq, int Lk, int D, const int64_t q_strides[3],
+                             const int64_t k_strides[3], const int64_t v_strides[3],
+                             const int64_t o_strides[3], float sm_scale, void* stream);
+
 /*
  * The per-token Q quantizer of dc_int8_attn_fwd (the same device code), with
  * its codes written out for verification: q8 int8 [B, H, Lq32, Dp] and

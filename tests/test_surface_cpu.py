@@ -248,6 +248,10 @@ def test_argument_checks_fail_before_any_launch():
     assert qk(_lib.BF16, 1, 64, wdt=_lib.F16) == 1 and b"weight_dtype" in so.dc_last_error()
     assert qk(_lib.BF16, 1, 64, flags=4) == 1 and b"flags" in so.dc_last_error()
     assert qk(_lib.BF16, 1, 64, eps=-1.0) == 1 and b"eps" in so.dc_last_error()
+    # dc_int8_attn_fwd_noalloc: a call beyond its scratch is refused before any HIP call
+    assert so.dc_int8_attn_fwd_noalloc(16, 16, 16, 16, _lib.BF16, 8, 32, 8192, 8192, 128, st, st, st, st, 0.1,
+                                       None) == 4
+    assert b"scratch" in so.dc_last_error()
     # dc_rescale: M or N beyond int range is rejected (the kernel indexes rows in int)
     assert so.dc_rescale(16, 4, 16, 16, None, -1, 16, _lib.BF16, 4, (1 << 31) + 5, 4, None) == 1
     assert b"too large" in so.dc_last_error()
