@@ -764,6 +764,274 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs p) {
   attn_merge_tile<DT, DP>(p, blockIdx.x, lds);
 }
 
+
+// ---------------------------------------------------------------- 3b. attention for D > 64: DMA-fed, 256 queries per workgroup
+//
+// attn_wide_kernel: head dims 65 .. 128 (Dp = 128), key ranges up to
+// WIDE_MAX_TILES tiles. A workgroup owns 256 query rows of one (b, h): 8 waves
+// of 32 rows, two per SIMD, all fed by one stream of K / V tiles. K (int8,
+// from the workspace) and V (16-bit, read in place) go from global memory
+// straight into LDS (global_load_lds: no staging registers, no LDS store
+// instructions) through a ring of ATTN_WIDE_STAGES stages of one 64-key tile
+// each, loaded 3 tiles ahead. Instead of padded rows, XOR swizzles keep the
+// operand reads conflict-free (0 bank conflicts counted):
+//   K row r (128 B): 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7), so the
+//     16 rows one ds_read_b128 serves per cycle cover all banks;
+//   V row r (256 B): 64-byte segment g stored at segment g ^ (r & 3), so the
+//     4 rows a 16-lane ds_read_b64_tr_b16 group reads lie in 4 different
+//     segments.
+// The K block scales are staged in LDS once, so no global load sits in the
+// loop (a uniform load there would be ordered behind the tile loads and wait
+// for them). Same arithmetic as attn_kernel; the iteration is described at
+// `step` below.
+//
+// Measured on MI355X (FLUX shape): the kernel is bound by its instruction
+// stream, not by memory or synchronization. With the loads and barriers
+// removed it runs within 12% of its full time, and MFMA (31% busy) and VALU
+// (41% busy) work barely overlap on a SIMD: a microbenchmark of one tile's
+// mix (24 MFMAs, ~100 softmax VALU instructions) runs at about the sum of
+// the two alone however it is arranged.
+constexpr int BQW = 256;                            // query rows per workgroup
+constexpr int ATTN_WIDE_STAGES = 4;
+constexpr int WK_BYTES = BKEY * 128;                // int8 K tile
+constexpr int WV_BYTES = BKEY * 256;                // 16-bit V tile
+constexpr int WSTAGE = WK_BYTES + WV_BYTES;         // 24 KB
+constexpr int ATTN_WIDE_LDS = ATTN_WIDE_STAGES * WSTAGE;
+constexpr int WIDE_LOADS = 3;                       // DMA instructions per wave per tile: 1 K + 2 V
+constexpr int WIDE_MAX_TILES = 2048;                // K block scales staged in LDS: Lk <= 131072
+
+// vmcnt(n) with the other counters unconstrained (gfx9 encoding: vmcnt bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+#define DC_ATTN_WAIT_VMCNT(n_) __builtin_amdgcn_s_waitcnt(((n_) & 15) | (((n_) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr_t;
+
+// The 8 K operands (k-step ks, key block kb) of one 64-key tile from a
+// swizzled K stage; kfo[ks] is the lane's byte offset of its 16-byte chunk for
+// k-step ks (row l32).
+__device__ __forceinline__ void k_operands(const uint8_t* __restrict__ sK, const int (&kfo)[4], v4i (&ka)[8]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) ka[2 * ks + kb] = *reinterpret_cast<const v4i*>(sK + kfo[ks] + (32 * kb) * 128);
+}
+
+// S^T + magic from the K operands (`magic` holds MAGIC_I in every register: the
+// first k-step accumulates onto it, so the scores need no initialization).
+__device__ __forceinline__ void qk_mfma(const v4i (&ka)[8], const v4i (&qf)[4], const v16i& magic, v16i (&s)[2]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[2 * ks + kb], qf[ks], ks == 0 ? magic : s[kb], 0, 0, 0);
+}
+
+// V^T operand f (16-key step kk = f / 4, channel block i = f % 4) from a
+// swizzled V stage by two ds_read_tr16_b64; vfo[i] is the lane's byte offset
+// for channel block i (keys 4 hf + li / 4, + 8 for the second read).
+__device__ __forceinline__ v4i v_operand(const uint8_t* __restrict__ sV, const int (&vfo)[4], int f) {
+  const uint8_t* a = sV + vfo[f & 3] + (16 * (f >> 2)) * 256;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(const_cast<uint8_t*>(a)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(const_cast<uint8_t*>(a + 8 * 256)));
+  return v4i{(int)((uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16)),
+             (int)((uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16)),
+             (int)((uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16)),
+             (int)((uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16))};
+}
+
+// V operands are read VPRE MFMAs ahead of their use
+constexpr int VPRE = 4;
+
+template <int DT>
+__global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[ATTN_WIDE_LDS];
+  __shared__ float ks_l[WIDE_MAX_TILES];   // the (b, h)'s K block scales
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hf = lane >> 5, l32 = lane & 31;
+  const int nqt = (p.Lq + BQW - 1) / BQW;
+  const int qlog = xcd_order(blockIdx.x, gridDim.x);
+  const int qt = qlog % nqt, bh = qlog / nqt, b = bh / p.H, h = bh % p.H;
+  const int ntiles = p.Lk64 / BKEY;
+  const bool ragged = p.Lk % BKEY != 0;
+
+  // ---- DMA sources (byte offsets from the tile's first row). K: wave w
+  // loads rows 8 w + lane / 8, physical chunk lane % 8, logical chunk
+  // (lane % 8) ^ ((row >> 1) & 7). V: rows 4 (w + 8 u) + lane / 16 (u = 0, 1),
+  // physical chunk lane % 16, logical chunk (lane % 16) ^ ((row & 3) << 2),
+  // clamped to the last chunk inside D (channels past D feed O rows that are
+  // never stored).
+  const int8_t* kg = p.k8 + (int64_t)bh * p.Lk64 * 128;
+  const uint16_t* vg = static_cast<const uint16_t*>(p.v) + b * p.vsb + h * p.vsh;
+  const int krow = 8 * w + (lane >> 3);
+  const uint32_t koff = (uint32_t)(krow * 128 + 16 * ((lane & 7) ^ ((krow >> 1) & 7)));
+  int vrow[2], vcol[2];
+  uint32_t voff[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    vrow[u] = 4 * (w + 8 * u) + (lane >> 4);
+    vcol[u] = min((lane & 15) ^ ((vrow[u] & 3) << 2), p.D / 8 - 1) * 8;
+    voff[u] = (uint32_t)(vrow[u] * (int)p.vsl + vcol[u]) * 2u;   // the host keeps 64 V rows under 2^31 bytes
+  }
+  // tile `tile` into stage `st` (tile % STAGES); past the end the source is
+  // the last tile again (in bounds; that data is never read)
+  const uint8_t* kgw = reinterpret_cast<const uint8_t*>(kg) + koff;
+  auto issue = [&](int tile, int st) __attribute__((always_inline)) {
+    uint8_t* sb = lds + st * WSTAGE;
+    tile = min(tile, ntiles - 1);
+    __builtin_amdgcn_global_load_lds(kgw + tile * (BKEY * 128), (lds_void_ptr_t)(sb + 1024 * w), 16, 0, 0);
+    uint8_t* sv = sb + WK_BYTES;
+    if (ragged && tile == ntiles - 1) {
+      // keys past Lk read key Lk - 1 (their probabilities are 0; the values stay finite)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int key = min(tile * BKEY + vrow[u], p.Lk - 1);
+        __builtin_amdgcn_global_load_lds(vg + (int64_t)key * p.vsl + vcol[u],
+                                         (lds_void_ptr_t)(sv + 1024 * (w + 8 * u)), 16, 0, 0);
+      }
+    } else {
+      const uint8_t* vt = reinterpret_cast<const uint8_t*>(vg + (int64_t)tile * BKEY * p.vsl);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        __builtin_amdgcn_global_load_lds(vt + voff[u], (lds_void_ptr_t)(sv + 1024 * (w + 8 * u)), 16, 0, 0);
+    }
+  };
+
+  issue(0, 0);
+  issue(1, 1);
+  issue(2, 2);
+  // block scales into LDS (ordinary loads, waited for here, before any DMA
+  // wait counts rely on the load order)
+  for (int i = t; i < ntiles; i += 512) ks_l[i] = p.ks[(int64_t)bh * ntiles + i];
+
+  // ---- Q: the wave's 32 rows, quantized per token into MFMA B operands
+  v4i qf[4];
+  float cq;
+  const int qrow = qt * BQW + w * 32 + l32;
+  {
+    const bool valid = qrow < p.Lq;
+    const uint16_t* src = static_cast<const uint16_t*>(p.q) + b * p.qsb + (int64_t)(valid ? qrow : 0) * p.qsl + h * p.qsh;
+    cq = quantize_q_row<DT, 128>(src, valid, p.D, hf, qf) * p.scale_log2;
+  }
+
+  // ---- operand offsets. K (A of S^T = K Q^T): row 32 kb + l32, logical chunk
+  // 2 ks + hf, physical (2 ks + hf) ^ ((l32 >> 1) & 7) = 2 ks ^ (hf ^ ((l32 >> 1) & 7)).
+  const int kx = hf ^ ((l32 >> 1) & 7);
+  int kfo[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) kfo[ks] = l32 * 128 + 16 * ((2 * ks) ^ kx);
+  // V^T (A of O^T = V^T P^T) by ds_read_tr16_b64: 16-lane group g16 of half hf
+  // reads keys 16 kk + 4 hf + li / 4 (+ 8), channels 32 i + 16 g16 + 4 (li % 4);
+  // such a key's row has (row & 3) = li / 4, so channel block i sits at
+  // segment i ^ (li / 4)
+  const int li = lane & 15, g16 = (lane >> 4) & 1;
+  int vfo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vfo[i] = (4 * hf + (li >> 2)) * 256 + 64 * (i ^ (li >> 2)) + 32 * g16 + 8 * (li & 3);
+
+  float m = -INFINITY, lsum = 0.f;
+  v16f o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = v16f{0.f};
+  v16i magic;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) magic[j] = MAGIC_I;
+
+  // Iteration `tile` (its stage st = tile % STAGES, passed as a constant in
+  // the unrolled loop so every LDS address is a lane base plus an immediate).
+  // One barrier: before it each wave waits for its own loads of tile + 1;
+  // after it tile + 1 is complete in LDS for every wave, and every wave is
+  // done with tile - 1, whose stage receives tile + 3. Then the K operands of
+  // tile + 1 and the first V operands of tile are read (their latency runs
+  // under the row maxima); the row maxima of S(tile) (rescaling O when one
+  // grows); the QK^T MFMAs of tile + 1 into `nxt` interleaved with the
+  // exponentials of tile (at the last tile they recompute that tile's scores,
+  // never used, so the phase stays branch-free); the PV MFMAs of tile, each
+  // reading the V operand VPRE MFMAs ahead. TAIL: the ragged last tile.
+  auto step = [&](int tile, int st, v16i (&cur)[2], v16i (&nxt)[2], auto tail) __attribute__((always_inline)) {
+    constexpr bool TAIL = decltype(tail)::value;
+    DC_ATTN_WAIT_VMCNT(WIDE_LOADS);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(tile + 3, (st + 3) % ATTN_WIDE_STAGES);
+    const uint8_t* sv = lds + st * WSTAGE + WK_BYTES;
+    v4i ka[8], va[16];
+    k_operands(lds + ((st + 1) % ATTN_WIDE_STAGES) * WSTAGE, kfo, ka);
+#pragma unroll
+    for (int f = 0; f < VPRE; ++f) va[f] = v_operand(sv, vfo, f);
+    __builtin_amdgcn_sched_barrier(0);
+    const int key0 = tile * BKEY + 4 * hf;
+    float bias;
+    const float c = softmax_max<128, TAIL>(cur, key0, p.Lk, ks_l[tile], cq, m, lsum, o, bias);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t pk[2][8];
+    qk_mfma(ka, qf, magic, nxt);
+    softmax_exp<DT, TAIL>(cur, key0, p.Lk, c, bias, lsum, pk);
+    // the 8 QK^T MFMAs with 12 of the ~100 VALU instructions of the
+    // exponentials behind each
+#pragma unroll
+    for (int z = 0; z < 8; ++z) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // PV: MFMA f consumes V operand f, read VPRE MFMAs earlier
+#pragma unroll
+    for (int f = 0; f < 16; ++f) {
+      if (f + VPRE < 16) va[f + VPRE] = v_operand(sv, vfo, f + VPRE);
+      const int kk = f >> 2, kb = kk >> 1, j0 = 4 * (kk & 1);
+      const v4i pf = {(int)pk[kb][j0], (int)pk[kb][j0 + 1], (int)pk[kb][j0 + 2], (int)pk[kb][j0 + 3]};
+      o[f & 3] = mfma_pv<DT>(va[f], pf, o[f & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  v16i sa[2], sb[2];
+  // tile 0 complete for every wave; the block scales are in LDS
+  DC_ATTN_WAIT_VMCNT(2 * WIDE_LOADS);
+  __syncthreads();
+  {
+    v4i ka[8];
+    k_operands(lds, kfo, ka);
+    qk_mfma(ka, qf, magic, sa);
+  }
+  // the last tile of a ragged key range runs masked, after the others; the
+  // loop takes 4 tiles per trip (stages 0 .. 3 as constants), then 0 to 3 more
+  const int nfull = ragged ? ntiles - 1 : ntiles;
+  int tile = 0;
+  for (; tile + 4 <= nfull; tile += 4) {
+    step(tile, 0, sa, sb, std::false_type{});
+    step(tile + 1, 1, sb, sa, std::false_type{});
+    step(tile + 2, 2, sa, sb, std::false_type{});
+    step(tile + 3, 3, sb, sa, std::false_type{});
+  }
+  // remaining tiles: stage tile % 4 at run time, scores in sa
+  for (; tile < nfull; ++tile) {
+    step(tile, tile % ATTN_WIDE_STAGES, sa, sb, std::false_type{});
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
+  }
+  if (ragged) step(tile, tile % ATTN_WIDE_STAGES, sa, sb, std::true_type{});
+  // no load may still be writing this workgroup's LDS when it ends
+  DC_ATTN_WAIT_VMCNT(0);
+
+  // ---- epilogue: O / l (each lane half summed its own keys)
+  lsum += __shfl_xor(lsum, 32);
+  if (qrow < p.Lq) {
+    const float inv = 1.f / lsum;
+    uint16_t* dst = static_cast<uint16_t*>(p.o) + b * p.osb + (int64_t)qrow * p.osl + h * p.osh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * i + 8 * g + 4 * hf;
+        if (d >= p.D) continue;
+        const uint32_t lo = f32_to_h16<DT>(o[i][4 * g] * inv) | (f32_to_h16<DT>(o[i][4 * g + 1] * inv) << 16);
+        const uint32_t hi = f32_to_h16<DT>(o[i][4 * g + 2] * inv) | (f32_to_h16<DT>(o[i][4 * g + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(dst + d) = make_uint2(lo, hi);
+      }
+  }
+}
+#undef DC_ATTN_WAIT_VMCNT
+
 // ---------------------------------------------------------------- host
 
 // Attention workgroups resident at once on the current device (occupancy x
@@ -821,6 +1089,10 @@ static AttnPlan attn_plan(int64_t qtiles, int ntiles, int slots) {
 
 template <int DP>
 static AttnPlan attn_plan_dp(int dtype, int B, int H, int Lq, int Lk) {
+  if constexpr (DP == 128) {
+    // attn_wide_kernel: whole 256-row query tiles, no stream-K split
+    if ((Lk + BKEY - 1) / BKEY <= WIDE_MAX_TILES) return AttnPlan{(int)((int64_t)((Lq + BQW - 1) / BQW) * H * B), 0, 0};
+  }
   const int64_t qtiles = (int64_t)((Lq + BQ - 1) / BQ) * H * B;
   const int ntiles = (Lk + BKEY - 1) / BKEY;
   const int slots = dtype == DC_BF16 ? attn_slots<DC_BF16, DP>() : attn_slots<DC_F16, DP>();
@@ -856,6 +1128,12 @@ static int launch_attn(AttnArgs& a, hipStream_t st) {
   if (int e = launch_status("kstats_kernel")) return e;
   hipLaunchKernelGGL((kquant_kernel<DT, DP>), dim3(a.Lk64 / BKEY, a.H, a.B), dim3(256), 0, st, a);
   if (int e = launch_status("kquant_kernel")) return e;
+  if constexpr (DP == 128) {
+    if (a.Lk64 / BKEY <= WIDE_MAX_TILES) {
+      hipLaunchKernelGGL((attn_wide_kernel<DT>), dim3((unsigned)a.dp_blocks), dim3(512), 0, st, a);
+      return launch_status("attn_wide_kernel");
+    }
+  }
   hipLaunchKernelGGL((attn_kernel<DT, DP>), dim3((unsigned)(a.dp_blocks + a.sk_blocks)), dim3(256), 0, st, a);
   if (int e = launch_status("attn_kernel")) return e;
   if (a.sk_blocks == 0) return DC_OK;

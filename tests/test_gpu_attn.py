@@ -57,6 +57,8 @@ CASES = [
     # extensions: bf16 (FLUX), head dim 64 (SDXL), 40 (SD1.5, padded to 64)
     (1, 1024, 1024, 4, 128, torch.bfloat16), (2, 300, 500, 3, 64, torch.float16),
     (2, 257, 77, 2, 40, torch.float16), (1, 333, 190, 2, 40, torch.bfloat16),
+    # head dims between 64 and 128 (padded to 128; V channels past D clamped in the loads)
+    (1, 300, 333, 2, 96, torch.bfloat16), (2, 513, 129, 3, 72, torch.float16),
 ]
 
 
@@ -142,12 +144,13 @@ def test_deterministic(gpu):
 
 @pytest.mark.parametrize("B,H,L,D,dtype", [(2, 10, 4096, 64, torch.float16), (2, 10, 4096, 64, torch.bfloat16),
                                              (1, 24, 4096, 128, torch.bfloat16)])
+# (head dim 128 runs whole 256-row tiles without stream-K; it stays as a plain repeat test)
 def test_stream_k_repeat_calls_identical(gpu, B, H, L, D, dtype):
     """Launches with stream-K pieces and their merge give the same bits on
     every call (regression: the merge kernel once declared less LDS than its
     factor / 1 / l / slot layout uses, and tiles merged with another
     workgroup's factors now and then)."""
-    if A.attn_plan(B, H, L, L, D, dtype)["sk_blocks"] == 0:
+    if A.attn_plan(B, H, L, L, D, dtype)["sk_blocks"] == 0 and D <= 64:
         pytest.skip("no stream-K split at this shape on this device")
     g = torch.Generator(device=gpu).manual_seed(12)
     q = torch.randn(B, L, H, D, device=gpu, generator=g).to(dtype)
@@ -165,8 +168,8 @@ def test_stream_k_pieces_match_whole_tiles(gpu):
     same heads run whole (they differ only in where the running maximum sits
     when P is rounded to bf16), and the heads run whole in both launches are
     bit-identical."""
-    B, L, D, dtype = 1, 4096, 128, torch.bfloat16
-    H = 24
+    B, L, D, dtype = 1, 4096, 64, torch.float16
+    H = 20                       # SDXL's 2 x 10 heads at 4096 tokens: 640 query tiles, 512 run whole
     pl = A.attn_plan(B, H, L, L, D, dtype)
     per_head = L // 128
     if pl["sk_blocks"] == 0 or pl["dp_tiles"] % per_head:
