@@ -286,6 +286,7 @@ def shapes_report(dev):
     """One JSON line per BASELINE config shape: time, TOPS, % of peak, accuracy."""
     import torch.nn.functional as F
     from diffucore_amd import Int8Linear, attention_bhld, quantize_activation
+    from diffucore_amd._attention import SHORT_KEYS
     mixed_peak = 2.0 / (1.0 / INT8_PEAK_TOPS + 1.0 / 2500.0)
     g = torch.Generator(device=dev)
     for name, B, H, S, Skv, D, dt, koff in ATTN_SHAPES:
@@ -300,6 +301,7 @@ def shapes_report(dev):
         ms = per_call_ms(lambda: attention_bhld(q, k, v, "int8_turing"))
         ms_sdpa = per_call_ms(lambda: F.scaled_dot_product_attention(q, k, v))
         out = attention_bhld(q, k, v, "int8_turing")
+        route = "sdpa (short key range)" if Skv <= SHORT_KEYS else "int8"
         ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(B, S, H * D)
         ops = 4 * B * H * S * Skv * D
         tops = ops / (ms * 1e-3) / 1e12
@@ -307,7 +309,8 @@ def shapes_report(dev):
                           "dtype": str(dt)[6:], "ms": round(ms, 4), "TOPS": round(tops, 1),
                           "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
                           "pct_mixed_ceiling": round(100 * tops / mixed_peak, 2),
-                          "sdpa_ms": round(ms_sdpa, 4), "vs_fp32_sdpa": _cmp(out, ref)}), flush=True)
+                          "sdpa_ms": round(ms_sdpa, 4), "route": route, "vs_fp32_sdpa": _cmp(out, ref)}),
+              flush=True)
         del q, k, v, out, ref
     for name, M, K, N, dt in LIN_SHAPES:
         g.manual_seed(0)
@@ -383,6 +386,40 @@ def shapes_report(dev):
                           "speedup": round(ms_u / ms_f, 2), "fused_GBps": round(nbytes / (ms_f * 1e-3) / 1e9, 1)}),
               flush=True)
         del h, pre
+    # GEGLU middle (DC_ACT_GEGLU) against the unfused ops, at SDXL's feed-forward shapes
+    for name, M, N in (("sdxl_geglu_middle_4096", 8192, 5120), ("sdxl_geglu_middle_1024", 2048, 10240)):
+        g.manual_seed(0)
+        h = (torch.randn(M, 2 * N, generator=g, device=dev) * 2).to(torch.float16)
+
+        def unfused_geglu():
+            a, gate = h.chunk(2, dim=-1)
+            return quantize_activation(a * F.gelu(gate), 256)
+
+        ms_u = per_call_ms(unfused_geglu)
+        ms_f = per_call_ms(lambda: act_quantize(h, 256, "geglu"))
+        nbytes = M * 2 * N * 2 + M * N + 4 * M
+        print(json.dumps({"kind": "fused_geglu_middle", "shape": name, "M": M, "N": N, "dtype": "float16",
+                          "unfused_ms": round(ms_u, 4), "fused_ms": round(ms_f, 4),
+                          "speedup": round(ms_u / ms_f, 2), "fused_GBps": round(nbytes / (ms_f * 1e-3) / 1e9, 1)}),
+              flush=True)
+        del h
+    # the UNet transformer block (unet_block.py) at SD1.5 / SDXL shapes: fp16 eager against W8A8 + INT8
+    import copy
+    import unet_block as UB
+    for lv in UB.LEVELS:
+        blk = UB.build(lv, dev)
+        x, ctx = UB.inputs(lv, dev)
+        with torch.no_grad():
+            ms_e = per_call_ms(lambda: blk(x, ctx))
+            ref = blk(x, ctx) - x
+            qb = UB.to_int8(copy.deepcopy(blk), dev)
+            ms_q = per_call_ms(lambda: qb(x, ctx))
+            out = qb(x, ctx) - x
+        print(json.dumps({"kind": "unet_block", "shape": lv.name, "B": lv.batch, "tokens": lv.tokens, "dim": lv.dim,
+                          "heads": lv.heads, "ctx": [lv.ctx_len, lv.ctx_dim], "dtype": "float16",
+                          "fp16_eager_ms": round(ms_e, 4), "int8_ms": round(ms_q, 4),
+                          "speedup": round(ms_e / ms_q, 2), "update_vs_fp16": _cmp(out, ref)}), flush=True)
+        del blk, qb, x, ctx, ref, out
     # QK RMSNorm + rotary (dc_qk_norm_rope) against FLUX's eager ops, at the FLUX double-block shape:
     # txt (512) and img (4096) q/k/v views of the two qkv projections -> joint (B, H, L, D) q, k, v
     import flux_step as FS

@@ -136,6 +136,23 @@ def test_other_head_dims_fall_back_to_sdpa(gpu):
         assert torch.equal(A.attention_blhd(q, q, q, "int8_turing"), A.attention_blhd(q, q, q, "sdpa"))
 
 
+def test_short_key_ranges_take_sdpa(gpu):
+    """Key ranges of at most SHORT_KEYS (cross-attention over a 77-token text
+    context) run exact SDPA on the int8_turing backend, as a UNet stamps it
+    on its cross-attention too (unet.py:122-145 has no is_selfattn); one key
+    more runs the INT8 kernels, within the reference's bar."""
+    torch.manual_seed(1)
+    q = torch.randn(2, 8, 4096, 40, device=gpu).half()                  # SD1.5 level-1 cross-attention
+    for lk in (77, A.SHORT_KEYS):
+        k, v = (torch.randn(2, 8, lk, 40, device=gpu).half() for _ in range(2))
+        assert torch.equal(A.attention_bhld(q, k, v, "int8_turing"), A.attention_bhld(q, k, v, "sdpa"))
+    k, v = (torch.randn(2, 8, A.SHORT_KEYS + 1, 40, device=gpu).half() for _ in range(2))
+    out = A.attention_bhld(q, k, v, "int8_turing")
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(2, 4096, -1)
+    assert not torch.equal(out, A.attention_bhld(q, k, v, "sdpa"))
+    assert rel_l2(np32(out), np32(ref)) < 3e-2 and cosine(np32(out), np32(ref)) > 0.9995
+
+
 def test_deterministic(gpu):
     q, k, v = _inputs(1, 500, 700, 3, 128, torch.bfloat16, seed=3)
     outs = [_run(q, k, v, gpu)[0] for _ in range(3)]
