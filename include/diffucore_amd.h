@@ -197,12 +197,14 @@ size_t dc_int8_attn_workspace_bytes(int B, int H, int Lq, int Lk, int D);
 /*
  * How dc_int8_attn_fwd splits its work at this shape on the current device
  * (no counterpart in the reference, whose grid is one CTA per 128-query tile,
- * int8_attn_sm80.cu:486-494; for profiling and tests). The 128-query tiles
- * (b, h, tile) in that order fill whole rounds of the device's resident
- * workgroups, *dp_tiles of them, each run whole; the remaining *sk_tiles
- * tiles' (query tile, 64-key tile) pairs are shared by *sk_blocks stream-K
- * workgroups (0 when the last round is run whole) whose partial results a
- * merge kernel combines. Returns 0, or DC_EINVAL for a bad shape or dtype.
+ * int8_attn_sm80.cu:486-494; for profiling and tests). Head dims up to 64: the
+ * 128-query tiles (b, h, tile) in that order fill whole rounds of the
+ * device's resident workgroups, *dp_tiles of them, each run whole; the
+ * remaining *sk_tiles tiles' (query tile, 64-key tile) pairs are shared by
+ * *sk_blocks stream-K workgroups (0 when the last round is run whole) whose
+ * partial results a merge kernel combines. Head dims above 64 (key ranges up
+ * to 131072): *dp_tiles 256-query tiles, all run whole. Returns 0, or
+ * DC_EINVAL for a bad shape or dtype.
  */
 int dc_int8_attn_plan(int dtype, int B, int H, int Lq, int Lk, int D, int* dp_tiles, int* sk_blocks,
                       int* sk_tiles);
