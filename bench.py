@@ -34,6 +34,7 @@ The same run also measures, and adds to the JSON line:
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -210,6 +211,7 @@ def cpu_baseline(shape, budget_s: float = 12.0, rows: int = 256):
         if el >= budget_s:
             break
     tops = done * ops_per / el / 1e12
+    cfg1 = cpu_cfg1()
     cpu = platform.processor() or "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -224,7 +226,84 @@ def cpu_baseline(shape, budget_s: float = 12.0, rows: int = 256):
                    f"one double + one single FLUX block with {rows} activation rows per linear and {rows} "
                    f"queries x {L} keys x {H} heads per attention, {done} repetitions in {el:.1f} s; "
                    f"cpu '{cpu}', os.cpu_count()={os.cpu_count()}"),
+        "cfg1": cfg1,
     }
+
+
+def gemm_source_sha256() -> str:
+    return hashlib.sha256((ROOT / "diffucore_amd" / "csrc" / "gemm.hip").read_bytes()).hexdigest()
+
+
+def traffic_summary(root: Path) -> None:
+    """Per-dispatch HBM traffic from rocprofv3 --pmc runs (one counter each):
+    root/copy_FETCH_SIZE, root/copy_WRITE_SIZE (a 1 GiB device copy, from
+    --copy-calibration) calibrate the counters; root/step_FETCH_SIZE,
+    root/step_WRITE_SIZE (one hot-path step) are averaged per kernel and
+    scaled. Writes profiles/gemm_flux_step_traffic.json, stamped with the GEMM
+    source's hash so bench runs on other sources leave `traffic` null."""
+    import csv
+    import glob
+
+    def per_kernel(d):
+        acc = {}
+        for f in glob.glob(str(root / d / "**" / "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                a = acc.setdefault(r["Kernel_Name"], [0.0, 0])
+                a[0] += float(r["Counter_Value"])
+                a[1] += 1
+        return {k: (v[0] / v[1], v[1]) for k, v in acc.items()}
+
+    cf, cw = per_kernel("copy_FETCH_SIZE"), per_kernel("copy_WRITE_SIZE")
+    copy_k = next(k for k in cf if "copyBuffer" in k)
+    copy_bytes = 1024 << 20
+    fetch_scale = copy_bytes / (cf[copy_k][0] * 1024)
+    write_scale = copy_bytes / (cw[copy_k][0] * 1024)
+    sf, sw = per_kernel("step_FETCH_SIZE"), per_kernel("step_WRITE_SIZE")
+    kernels = {}
+    for k in sf:
+        if "dc::" not in k:
+            continue
+        name = k.split("(")[0].replace("void ", "")
+        kernels[name] = {"dispatches": sf[k][1], "fetch_bytes": int(sf[k][0] * 1024 * fetch_scale),
+                         "write_bytes": int(sw.get(k, (0, 0))[0] * 1024 * write_scale)}
+    dma = next(v for k, v in kernels.items() if "w8a8_gemm_dma_kernel" in k)
+    out = {"kernel": next(k for k in kernels if "w8a8_gemm_dma_kernel" in k),
+           "hbm_bytes_per_launch": dma["fetch_bytes"] + dma["write_bytes"],
+           "fetch_bytes_per_launch": dma["fetch_bytes"], "write_bytes_per_launch": dma["write_bytes"],
+           "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
+           "calibration": f"1 GiB device copy: FETCH_SIZE {cf[copy_k][0]:.1f} KiB, WRITE_SIZE {cw[copy_k][0]:.1f} "
+                          f"KiB per dispatch",
+           "kernel_source_sha256": gemm_source_sha256(), "per_kernel": kernels}
+    (ROOT / "profiles" / "gemm_flux_step_traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps({k: out[k] for k in ("kernel", "hbm_bytes_per_launch", "fetch_scale", "write_scale")}))
+
+
+def cpu_cfg1(budget_s: float = 4.0):
+    """BASELINE config 1 on the reference's CPU path: W8A8 linear on x fp32
+    [8192, 320] ~N(0, 1) with 2 of 320 channels (0.5%) scaled x20 as outliers,
+    W [1280, 320] ~N(0, 0.02), per-token int8 activations, per-channel int8
+    weights, group 0, int32 accumulate, fp32 out, seed 0 (generator draws:
+    x, outlier channels, W). Timed over ``budget_s`` on all host threads."""
+    from oracle import cpu_path as C
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(8192, 320, generator=g)
+    x[:, torch.randperm(320, generator=g)[:2]] *= 20
+    w = torch.randn(1280, 320, generator=g) * 0.02
+    q, s = C.quantize_rows(w)
+    C.w8a8_linear(x, q, s, None, 0)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        C.w8a8_linear(x, q, s, None, 0)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    ms = el / n * 1e3
+    return {"what": "W8A8 linear x fp32 [8192,320] (0.5% outlier channels x20), W [1280,320], group 0, fp32 out: "
+                    "quantize_rows -> torch._int_mm -> rescale on the CPU",
+            "ms_per_call": round(ms, 3), "TOPS": round(2 * 8192 * 1280 * 320 / (ms * 1e-3) / 1e12, 4),
+            "cores": torch.get_num_threads(), "calls": n}
 
 
 # ---------------------------------------------------------------- per-shape report
@@ -475,7 +554,13 @@ def main():
                     help="only run a 1 GiB device copy (scales the rocprofv3 byte counters) and exit")
     ap.add_argument("--shapes", action="store_true",
                     help="only print the per-shape report (every BASELINE config shape) and exit")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="only summarize rocprofv3 FETCH_SIZE / WRITE_SIZE runs under DIR (copy_* and step_*) "
+                         "into profiles/gemm_flux_step_traffic.json and exit (no GPU)")
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_summary(Path(args.traffic_from))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
               "run it with --gpus 1.", file=sys.stderr)
@@ -568,15 +653,21 @@ def main():
     bytes_per_launch = g["bytes"] / g["launches"]
     launch_s = g["ms"] / g["launches"] * 1e-3
     achieved = ops_per_launch / launch_s / 1e12
-    traffic = None
+    # HBM bytes per launch from the committed counter summary, used only when it
+    # was measured on the GEMM source this run executes
+    traffic, traffic_src = None, {"profile": "profiles/gemm_flux_step_traffic.json"}
     tfile = ROOT / "profiles" / "gemm_flux_step_traffic.json"
     if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        tj = json.loads(tfile.read_text())
+        traffic_src["kernel_source_sha256"] = tj.get("kernel_source_sha256")
+        traffic_src["matches_current_source"] = tj.get("kernel_source_sha256") == gemm_source_sha256()
+        if traffic_src["matches_current_source"]:
+            traffic = tj.get("hbm_bytes_per_launch")
     roofline = {"kernel": "w8a8_gemm_dma_kernel (256x256 tiles, 4 waves, operands loaded straight into LDS): the "
                           f"{g['launches'] // args.steps} FLUX-step launches it runs (img MLP up, single linear1 "
                           "and linear2)",
                 "bound": "mfma", "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": traffic,
+                "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "algorithmic_ops_per_launch": int(ops_per_launch),
                 "algorithmic_bytes_per_launch": int(bytes_per_launch),
                 "avg_launch_us": round(1e6 * launch_s, 2),
