@@ -202,8 +202,10 @@ size_t dc_int8_attn_workspace_bytes(int B, int H, int Lq, int Lk, int D);
  * device's resident workgroups, *dp_tiles of them, each run whole; the
  * remaining *sk_tiles tiles' (query tile, 64-key tile) pairs are shared by
  * *sk_blocks stream-K workgroups (0 when the last round is run whole) whose
- * partial results a merge kernel combines. Head dims above 64 (key ranges up
- * to 131072): *dp_tiles 256-query tiles, all run whole. Returns 0, or
+ * partial results a merge kernel combines. Head dims above 64: 256-query
+ * tiles, all run whole (*dp_tiles of them, *sk_blocks = *sk_tiles = 0), when
+ * there are at least as many as the device has compute units and the key
+ * range is at most 131072; otherwise the 128-query split above. Returns 0, or
  * DC_EINVAL for a bad shape or dtype.
  */
 int dc_int8_attn_plan(int dtype, int B, int H, int Lq, int Lk, int D, int* dp_tiles, int* sk_blocks,

@@ -60,6 +60,24 @@ CASES = [
     # head dims between 64 and 128 (padded to 128; V channels past D clamped in the loads)
     (1, 300, 333, 2, 96, torch.bfloat16), (2, 513, 129, 3, 72, torch.float16),
 ]
+# grids of at least one 256-query tile per CU, which run the 8-wave DMA-fed
+# kernel: head dims 128 / 96 / 72, ragged key ranges, a ragged last query tile
+WIDE_CASES = [
+    (1, 1024, 300, 64, 128, torch.bfloat16), (2, 1024, 333, 64, 96, torch.float16),
+    (1, 1200, 129, 52, 72, torch.bfloat16),
+]
+CASES += WIDE_CASES
+
+
+@pytest.mark.parametrize("B,Lq,Lk,H,D,dtype", WIDE_CASES)
+def test_wide_cases_run_256_query_tiles(gpu, B, Lq, Lk, H, D, dtype):
+    """On MI355X (256 CUs) these shapes take whole 256-query tiles; the small
+    head-dim-128 shapes above take 128-query tiles."""
+    if torch.cuda.get_device_properties(gpu).multi_processor_count != 256:
+        pytest.skip("tile counts are for 256 CUs")
+    assert A.attn_plan(B, H, Lq, Lk, D, dtype) == {"dp_tiles": (Lq + 255) // 256 * B * H, "sk_blocks": 0,
+                                                   "sk_tiles": 0}
+    assert A.attn_plan(1, 4, 1024, 1024, 128, dtype) == {"dp_tiles": 32, "sk_blocks": 0, "sk_tiles": 0}
 
 
 @pytest.mark.parametrize("B,Lq,Lk,H,D,dtype", CASES)

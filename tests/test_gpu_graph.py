@@ -7,8 +7,9 @@ captured input buffers must reach the next replay.
 
 Covered: the quantize kernel, each GEMM plan the FLUX step uses (DMA-fed
 256 x 256, 192 x 256 / 128 x 128, split-K with its workspace and epilogue
-pass) and the INT8 attention (K statistics, K quantize, attention; stream-K
-pieces and their merge at the FLUX shape).
+pass) and the INT8 attention (K statistics, K quantize, attention): the
+256-query kernel at the FLUX shape, stream-K pieces and their merge at SDXL's
+4096-token self-attention, and the 128-query kernel whole.
 """
 
 from __future__ import annotations
@@ -24,7 +25,7 @@ pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
 # (M, K, N): DMA-fed 256 x 256 plan, split-K (M = 512, K = 3072), a ragged one
 LINEARS = [(4096, 512, 4096), (512, 3072, 3072), (1000, 768, 1280)]
-ATTN = [(1, 24, 4608, 128), (1, 4, 1000, 64)]
+ATTN = [(1, 24, 4608, 128), (2, 10, 4096, 64), (1, 4, 1000, 64)]
 
 
 def _case(gpu, seed):

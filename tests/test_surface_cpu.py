@@ -303,10 +303,12 @@ def test_attention_work_split_without_a_gpu():
     per CU on 256 CUs, when no device answers). SDXL's 640 query tiles at 4096
     tokens run 512 whole and share the last 128 (a quarter-full round) over
     512 stream-K workgroups; whole rounds and short key ranges run whole.
-    Head dims above 64 run 256-query tiles, all whole (FLUX: 18 per head)."""
+    Head dims above 64 run 256-query tiles, all whole (FLUX: 18 per head),
+    when there are at least as many as CUs; fewer take 128-query tiles."""
     from diffucore_amd import _attention as A
     assert A.attn_plan(2, 10, 4096, 4096, 64, torch.float16) == {"dp_tiles": 512, "sk_blocks": 512, "sk_tiles": 128}
     assert A.attn_plan(1, 24, 4608, 4608, 128) == {"dp_tiles": 432, "sk_blocks": 0, "sk_tiles": 0}
+    assert A.attn_plan(1, 4, 1024, 1024, 128) == {"dp_tiles": 32, "sk_blocks": 0, "sk_tiles": 0}
     assert A.attn_plan(2, 8, 4096, 4096, 40, torch.float16) == {"dp_tiles": 512, "sk_blocks": 0, "sk_tiles": 0}
     assert A.attn_plan(2, 10, 4096, 77, 64, torch.float16)["sk_blocks"] == 0
     ws = _lib.lib().dc_int8_attn_workspace_bytes(2, 10, 4096, 4096, 64)
