@@ -5,7 +5,9 @@ A step is one pass of the hot path of one FLUX.1-schnell denoise step at
 19 double-stream blocks (img/txt qkv, joint INT8 attention, img/txt proj,
 img/txt MLP up and down) and 38 single-stream blocks (linear1, INT8 attention,
 linear2). Every linear is a W8A8 ``Int8Linear`` with its own random weights
-(quantize kernel + fused-epilogue GEMM); every attention is
+(quantize kernel + fused-epilogue GEMM; a double block's img linear and its
+txt twin share one grouped GEMM launch where the library's plan expects that
+to pay, as flux_step runs them); every attention is
 ``attention_bhld(..., "int8_turing")``. Algorithmic work is 74.36 TOP per
 step (GEMM 2*M*N*K, attention 4*B*H*S^2*D). Inputs are resident in HBM.
 
@@ -86,22 +88,31 @@ class HotPath:
             x = self.acts[key]
             return ("gemm", layer, x, 2 * x.shape[0] * layer.out_features * layer.in_features)
 
+        def pair(la, ka, lb, kb):
+            # a double block's img linear and its txt twin: one grouped launch
+            # when the library's plan expects it to pay, as flux_step runs them
+            xa, xb = self.acts[ka], self.acts[kb]
+            if _int8.gemm_group_plan([xa.shape[0], xb.shape[0]], la.out_features, la.in_features):
+                return [("group", (la, lb), (xa, xb), 2 * (xa.shape[0] + xb.shape[0]) * la.out_features * la.in_features)]
+            return [lin(la, ka), lin(lb, kb)]
+
         for blk in model.double_blocks:
-            for layer, key in ((blk.img_qkv, "img"), (blk.txt_qkv, "txt")):
-                self.ops.append(lin(layer, key))
+            self.ops += pair(blk.img_qkv, "img", blk.txt_qkv, "txt")
             self.ops.append(("attn", None, None, attn_ops))
-            for layer, key in ((blk.img_proj, "img"), (blk.txt_proj, "txt"), (blk.img_mlp[0], "img"),
-                               (blk.img_mlp[2], "img_h"), (blk.txt_mlp[0], "txt"), (blk.txt_mlp[2], "txt_h")):
-                self.ops.append(lin(layer, key))
+            self.ops += pair(blk.img_proj, "img", blk.txt_proj, "txt")
+            self.ops += pair(blk.img_mlp[0], "img", blk.txt_mlp[0], "txt")
+            self.ops += pair(blk.img_mlp[2], "img_h", blk.txt_mlp[2], "txt_h")
         for blk in model.single_blocks:
             self.ops.append(lin(blk.linear1, "x"))
             self.ops.append(("attn", None, None, attn_ops))
             self.ops.append(lin(blk.linear2, "x_h"))
         assert all(isinstance(op[1], _int8.Int8Linear) for op in self.ops if op[0] == "gemm")
+        assert all(isinstance(la, _int8.Int8Linear) for op in self.ops if op[0] == "group" for la in op[1])
         self.total_ops = sum(op[3] for op in self.ops)
-        # which GEMM kernel each linear runs (dc_w8a8_gemm_plan)
-        self.plans = [_int8.gemm_plan(op[2].shape[0], op[1].out_features, op[1].in_features)
-                      if op[0] == "gemm" else None for op in self.ops]
+        # which GEMM kernel each launch runs (dc_w8a8_gemm_plan; grouped
+        # launches always run the DMA-fed 256 x 256 kernel)
+        self.plans = [_int8.gemm_plan(op[2].shape[0], op[1].out_features, op[1].in_features) if op[0] == "gemm"
+                      else "dma_256x256" if op[0] == "group" else None for op in self.ops]
         self.ws = None
 
     def run(self, recs=None):
@@ -115,11 +126,28 @@ class HotPath:
             for kind, layer, x, _ in self.ops:
                 if kind == "gemm":
                     layer.matmul_quantized(*_int8.quantize_activation(x, layer.group), x.dtype)
+                elif kind == "group":
+                    qs = [_int8.quantize_activation(xi, li.group) for li, xi in zip(layer, x)]
+                    _int8.matmul_quantized_group([(li, *qi) for li, qi in zip(layer, qs)], x[0].dtype)
                 else:
                     attention_bhld(q, k, v, "int8_turing")
             return
         for (kind, layer, x, ops), plan in zip(self.ops, self.plans):
-            if kind == "gemm":
+            if kind == "group":
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(x) + 2)]
+                ev[0].record()
+                qs = []
+                for i, (li, xi) in enumerate(zip(layer, x)):
+                    qs.append(_int8.quantize_activation(xi, li.group))
+                    ev[i + 1].record()
+                    recs.append(("quant", ev[i], ev[i + 1], 0, xi.numel() * xi.element_size() + xi.numel() +
+                                 4 * xi.shape[0], None))
+                _int8.matmul_quantized_group([(li, *qi) for li, qi in zip(layer, qs)], x[0].dtype)
+                ev[-1].record()
+                K, N = layer[0].in_features, layer[0].out_features
+                gbytes = sum(xi.shape[0] * K + N * K + 4 * (xi.shape[0] + N) + 2 * N + 2 * xi.shape[0] * N for xi in x)
+                recs.append(("gemm", ev[len(x)], ev[-1], ops, gbytes, plan))
+            elif kind == "gemm":
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
                 e0.record()
                 qx, sx = _int8.quantize_activation(x, layer.group)
@@ -667,8 +695,9 @@ def main():
         if traffic_src["matches_current_source"]:
             traffic = tj.get("hbm_bytes_per_launch")
     roofline = {"kernel": "w8a8_gemm_dma_kernel (256x256 tiles, 4 waves, operands loaded straight into LDS): the "
-                          f"{g['launches'] // args.steps} FLUX-step launches it runs (img MLP up, single linear1 "
-                          "and linear2)",
+                          f"{g['launches'] // args.steps} FLUX-step launches it runs (img MLP up; the double blocks' "
+                          "img + txt qkv, proj and MLP down, each pair as one grouped launch; single linear1 and "
+                          "linear2)",
                 "bound": "mfma", "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                 "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "algorithmic_ops_per_launch": int(ops_per_launch),

@@ -48,6 +48,27 @@ struct GemmArgs {
   int64_t split_stride;
 };
 
+// One problem of a grouped launch (dc_w8a8_gemm_grouped): the per-problem
+// fields of GemmArgs.
+struct GroupProblem {
+  const int8_t* a;
+  const int8_t* w;
+  const float* sx;
+  const float* sw;
+  const void* bias;
+  void* out;
+  int64_t lda, ldw, ldo;
+  int M, tiles_m, vec_out, vec16;
+};
+
+// A grouped launch of the DMA-fed kernel: problem g owns logical tiles
+// first[g] .. first[g + 1] - 1. ngroup == 0: one problem, all in GemmArgs.
+struct GroupArgs {
+  int ngroup;
+  int first[DC_GEMM_MAX_GROUP + 1];
+  GroupProblem prob[DC_GEMM_MAX_GROUP];
+};
+
 constexpr int BK = 128;            // k bytes per LDS stage
 constexpr int PITCH = BK + 16;     // padded LDS row (bytes)
 constexpr int GROUP_M = 8;
@@ -120,15 +141,44 @@ struct Tile {
 
 // Tile order: XCD-contiguous ranges of workgroups (the hardware deals them
 // round-robin over the 8 XCDs), then GROUP_M m-tiles per sweep along n.
-__device__ __forceinline__ void tile_origin(const GemmArgs& p, int BM, int BN, int& m0, int& n0) {
+
+// Workgroup blockIdx.x's logical tile.
+__device__ __forceinline__ int xcd_logical() {
   const int nwg = gridDim.x, wg = blockIdx.x;
-  const int logical = (nwg % 8 == 0) ? (wg % 8) * (nwg / 8) + wg / 8 : wg;
-  const int per_group = GROUP_M * p.tiles_n;
+  return (nwg % 8 == 0) ? (wg % 8) * (nwg / 8) + wg / 8 : wg;
+}
+
+// Origin of logical tile `logical` of a tiles_m x tiles_n grid: GROUP_M
+// m-tiles per sweep along n.
+__device__ __forceinline__ void tile_coords(int logical, int tiles_m, int tiles_n, int BM, int BN, int& m0, int& n0) {
+  const int per_group = GROUP_M * tiles_n;
   const int grp = logical / per_group;
   const int first_m = grp * GROUP_M;
-  const int gsize = min(p.tiles_m - first_m, GROUP_M);
+  const int gsize = min(tiles_m - first_m, GROUP_M);
   m0 = (first_m + (logical % per_group) % gsize) * BM;
   n0 = ((logical % per_group) / gsize) * BN;
+}
+
+__device__ __forceinline__ void tile_origin(const GemmArgs& p, int BM, int BN, int& m0, int& n0) {
+  tile_coords(xcd_logical(), p.tiles_m, p.tiles_n, BM, BN, m0, n0);
+}
+
+// Grouped launch: the problem that owns this workgroup's logical tile, its
+// fields copied into p (every index a constant: no dynamic indexing of the
+// kernel arguments), and the tile's origin in that problem.
+static_assert(DC_GEMM_MAX_GROUP == 4, "group_origin selects among 4 problems");
+__device__ __forceinline__ void group_origin(GemmArgs& p, const GroupArgs& g, int BM, int BN, int& m0, int& n0) {
+  const int logical = xcd_logical();
+  const int k = (g.ngroup > 3 && logical >= g.first[3]) ? 3
+              : (g.ngroup > 2 && logical >= g.first[2]) ? 2
+              : (g.ngroup > 1 && logical >= g.first[1]) ? 1 : 0;
+#define DC_SEL(f_) (k == 0 ? g.prob[0].f_ : k == 1 ? g.prob[1].f_ : k == 2 ? g.prob[2].f_ : g.prob[3].f_)
+  p.a = DC_SEL(a); p.w = DC_SEL(w); p.sx = DC_SEL(sx); p.sw = DC_SEL(sw); p.bias = DC_SEL(bias);
+  p.out = DC_SEL(out); p.lda = DC_SEL(lda); p.ldw = DC_SEL(ldw); p.ldo = DC_SEL(ldo);
+  p.M = DC_SEL(M); p.tiles_m = DC_SEL(tiles_m); p.vec_out = DC_SEL(vec_out); p.vec16 = DC_SEL(vec16);
+  const int first = k == 0 ? g.first[0] : k == 1 ? g.first[1] : k == 2 ? g.first[2] : g.first[3];
+#undef DC_SEL
+  tile_coords(logical - first, p.tiles_m, p.tiles_n, BM, BN, m0, n0);
 }
 
 // Stores one workgroup tile from its MFMA accumulators (C^T layout): register
@@ -480,7 +530,7 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 #define DC_WAIT_VMCNT_LGKM0(n_) __builtin_amdgcn_s_waitcnt(((n_) & 15) | (((n_) >> 4) << 14) | (7 << 4))
 
 template <int OUT_DT, int BIAS_DT>
-__global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p, GroupArgs g) {
   constexpr int BN = 256, BM = 256, FN = 4, FM = 4;
   __shared__ __attribute__((aligned(1024))) uint8_t st0[DSTAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[DSTAGE];
@@ -492,7 +542,8 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p) {
   const int l32 = lane & 31, hf = lane >> 5;
   const int wn = w & 1, wm = w >> 1;
   int m0, n0;
-  tile_origin(p, BM, BN, m0, n0);
+  if (g.ngroup > 0) group_origin(p, g, BM, BN, m0, n0);
+  else tile_origin(p, BM, BN, m0, n0);
 
   float* sw_l = epi_v;
   float* b_l = epi_v + BN;
@@ -706,7 +757,15 @@ static int launch_gemm_dma(GemmArgs p, hipStream_t st) {
   p.tiles_m = (p.M + 255) / 256;
   const int64_t tiles = (int64_t)p.tiles_n * p.tiles_m;
   if (tiles > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm: problem too large");
-  hipLaunchKernelGGL((w8a8_gemm_dma_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)tiles), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((w8a8_gemm_dma_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)tiles), dim3(256), 0, st, p, GroupArgs{});
+  return launch_status("w8a8_gemm_dma_kernel");
+}
+
+// Grouped launch: g.first[g.ngroup] tiles in all (p holds N, K, tiles_n).
+template <int OUT_DT, int BIAS_DT>
+static int launch_gemm_dma_group(GemmArgs p, const GroupArgs& g, hipStream_t st) {
+  hipLaunchKernelGGL((w8a8_gemm_dma_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)g.first[g.ngroup]), dim3(256), 0, st, p,
+                     g);
   return launch_status("w8a8_gemm_dma_kernel");
 }
 
@@ -903,6 +962,102 @@ extern "C" int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
     case DC_BF16: return dispatch_bias<DC_BF16>(p, bias_dtype, st);
     case DC_F32: return dispatch_bias<DC_F32>(p, bias_dtype, st);
     default: return fail(DC_EINVAL, "dc_w8a8_gemm: bad out_dtype");
+  }
+}
+
+// ---------------------------------------------------------------- grouped launches
+
+template <int OUT_DT>
+static int group_bias(GemmArgs p, const GroupArgs& g, int bias_dtype, hipStream_t st) {
+  switch (bias_dtype) {
+    case DC_NONE: return launch_gemm_dma_group<OUT_DT, DC_NONE>(p, g, st);
+    case DC_F16: return launch_gemm_dma_group<OUT_DT, DC_F16>(p, g, st);
+    case DC_BF16: return launch_gemm_dma_group<OUT_DT, DC_BF16>(p, g, st);
+    default: return launch_gemm_dma_group<OUT_DT, DC_F32>(p, g, st);
+  }
+}
+
+static int64_t dma_tiles(int64_t M, int64_t N) { return ((M + 255) / 256) * ((N + 255) / 256); }
+
+extern "C" int dc_w8a8_gemm_group_plan(const int64_t* Ms, int count, int64_t N, int64_t K) {
+  clear_error();
+  if (!Ms || count < 1 || count > DC_GEMM_MAX_GROUP || N <= 0 || K <= 0) {
+    set_error("dc_w8a8_gemm_group_plan: bad arguments");
+    return -1;
+  }
+  int live = 0;
+  int64_t total = 0, largest = 0;
+  for (int i = 0; i < count; ++i) {
+    if (Ms[i] < 0) {
+      set_error("dc_w8a8_gemm_group_plan: negative M");
+      return -1;
+    }
+    if (Ms[i] == 0) continue;
+    ++live;
+    const int64_t t = dma_tiles(Ms[i], N);
+    total += t;
+    largest = t > largest ? t : largest;
+  }
+  if (K % (4 * DBK) || live < 2) return 0;
+  const int64_t cus = device_cus();
+  return (total + cus - 1) / cus <= (largest + cus - 1) / cus ? 1 : 0;
+}
+
+extern "C" int dc_w8a8_gemm_grouped(const dc_gemm_problem* problems, int count, int64_t N, int64_t K, int bias_dtype,
+                                    int out_dtype, void* stream) {
+  clear_error();
+  if (!problems) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: null pointer");
+  if (count < 1 || count > DC_GEMM_MAX_GROUP)
+    return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: count must be 1 .. DC_GEMM_MAX_GROUP");
+  if (N <= 0 || K <= 0) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: N and K must be positive");
+  if (N > 0x7fffffff || K > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: size too large");
+  if (K % (4 * DBK)) return fail(DC_EUNSUPPORTED, "dc_w8a8_gemm_grouped: needs K % 256 == 0");
+  if (out_dtype != DC_I32 && out_dtype != DC_F16 && out_dtype != DC_BF16 && out_dtype != DC_F32)
+    return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: bad out_dtype");
+  if (bias_dtype != DC_NONE && bias_dtype != DC_F16 && bias_dtype != DC_BF16 && bias_dtype != DC_F32)
+    return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: bad bias_dtype");
+  const int ob = elem_bytes(out_dtype);
+  GemmArgs p{};
+  p.N = (int)N;
+  p.K = (int)K;
+  p.tiles_n = (int)((N + 255) / 256);
+  GroupArgs g{};
+  int64_t tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    const dc_gemm_problem& q = problems[i];
+    if (q.M < 0) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: negative M");
+    if (q.M == 0) continue;
+    if (q.M > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: size too large");
+    if (!q.a || !q.w || !q.out) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: null pointer");
+    if (q.lda < K || q.ldw < K || q.lda % 16 || q.ldw % 16 || !aligned16(q.a) || !aligned16(q.w) ||
+        256 * q.lda >= (int64_t(1) << 31) || 256 * q.ldw >= (int64_t(1) << 31))
+      return fail(DC_EUNSUPPORTED,
+                  "dc_w8a8_gemm_grouped: needs lda, ldw >= K, multiples of 16 and below 2^23, 16-byte aligned a, w");
+    if (q.ldo < N) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: ldo < N");
+    if (out_dtype != DC_I32 && (!q.sx || !q.sw)) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: scales are required");
+    if (bias_dtype != DC_NONE && out_dtype != DC_I32 && !q.bias)
+      return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: bias_dtype given without bias");
+    GroupProblem& d = g.prob[g.ngroup];
+    d.a = q.a; d.w = q.w; d.sx = q.sx; d.sw = q.sw; d.bias = q.bias; d.out = q.out;
+    d.lda = q.lda; d.ldw = q.ldw; d.ldo = q.ldo;
+    d.M = (int)q.M;
+    d.tiles_m = (int)((q.M + 255) / 256);
+    d.vec_out = ((reinterpret_cast<uintptr_t>(q.out) % (4 * (uintptr_t)ob)) == 0) && (q.ldo % 4 == 0) &&
+                (out_dtype == DC_I32 || (reinterpret_cast<uintptr_t>(q.sw) & 15) == 0);
+    d.vec16 = d.vec_out && (reinterpret_cast<uintptr_t>(q.out) % 16) == 0 && (q.ldo * ob) % 16 == 0;
+    g.first[g.ngroup] = (int)tiles;
+    tiles += (int64_t)d.tiles_m * p.tiles_n;
+    if (tiles > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: problem too large");
+    ++g.ngroup;
+  }
+  if (g.ngroup == 0) return DC_OK;
+  g.first[g.ngroup] = (int)tiles;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case DC_I32: return launch_gemm_dma_group<DC_I32, DC_NONE>(p, g, st);
+    case DC_F16: return group_bias<DC_F16>(p, g, bias_dtype, st);
+    case DC_BF16: return group_bias<DC_BF16>(p, g, bias_dtype, st);
+    default: return group_bias<DC_F32>(p, g, bias_dtype, st);
   }
 }
 

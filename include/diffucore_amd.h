@@ -179,6 +179,48 @@ enum {
 int dc_w8a8_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw);
 
 /*
+ * Grouped W8A8 GEMM: up to DC_GEMM_MAX_GROUP problems that share N, K, the
+ * output dtype and the bias dtype, each with its own activations, weights,
+ * scales, bias and output, in one launch of the DMA-fed 256 x 256 kernel
+ * (their tiles back to back in one grid). Each output is bit-identical to
+ * dc_w8a8_gemm on the same problem. No counterpart in the reference, which
+ * runs each Int8Linear on its own (_int8.py:158-167); it is for callers that
+ * hold several independent linears of one shape at once, such as FLUX's
+ * double-stream blocks (flux_dit.py:275-330: the img and txt streams' qkv,
+ * proj and MLP-down layers), where a small problem's tiles then fill CUs the
+ * large one leaves idle in its last round.
+ * Needs K % 256 == 0 and, per problem, lda, ldw multiples of 16 with
+ * 256 * lda and 256 * ldw below 2^31, 16-byte aligned a and w, ldo >= N.
+ * Problems with M == 0 are skipped. No split-K: the workspace of dc_w8a8_gemm
+ * has no counterpart here.
+ */
+#define DC_GEMM_MAX_GROUP 4
+typedef struct dc_gemm_problem {
+  const int8_t* a;     /* [M, K] int8, row stride lda */
+  int64_t lda;
+  const int8_t* w;     /* [N, K] int8, row stride ldw */
+  int64_t ldw;
+  const float* sx;     /* [M] row scales (ignored for DC_I32 output) */
+  const float* sw;     /* [N] channel scales (ignored for DC_I32 output) */
+  const void* bias;    /* [N] of bias_dtype, or NULL with DC_NONE */
+  void* out;           /* [M, N] of out_dtype, row stride ldo */
+  int64_t ldo;
+  int64_t M;
+} dc_gemm_problem;
+int dc_w8a8_gemm_grouped(const dc_gemm_problem* problems, int count, int64_t N, int64_t K, int bias_dtype,
+                         int out_dtype, void* stream);
+
+/*
+ * Whether one dc_w8a8_gemm_grouped launch over problems of these row counts
+ * is expected to beat separate dc_w8a8_gemm calls on the current device: 1
+ * when K % 256 == 0, there are at least two non-empty problems and their
+ * 256 x 256 tiles together need no more rounds of the device's CUs than the
+ * largest problem's alone; 0 otherwise; -1 for bad arguments. No counterpart
+ * in the reference.
+ */
+int dc_w8a8_gemm_group_plan(const int64_t* Ms, int count, int64_t N, int64_t K);
+
+/*
  * The rescale pass on an int32 accumulator, for callers that hold one.
  * Replaces rescale (src/diffucore/models/_int8.py:313-323) and the Triton
  * _rescale_kernel (_int8.py:408-417). Same rounding as dc_w8a8_gemm.

@@ -50,7 +50,15 @@ afwd = sig("dc_int8_attn_fwd", I, [P, P, P, P, I, I, I, I, I, I, S3, S3, S3, S3,
 anoa = sig("dc_int8_attn_fwd_noalloc", I, [P, P, P, P, I, I, I, I, I, I, S3, S3, S3, S3, F, P])
 aws = sig("dc_int8_attn_workspace_bytes", SZ, [I] * 5)
 qq = sig("dc_int8_attn_quantize_q", I, [P, I, I, I, I, I, S3, P, P, P])
+class Prob(ctypes.Structure):
+    _fields_ = [("a", P), ("lda", I64), ("w", P), ("ldw", I64), ("sx", P), ("sw", P), ("bias", P), ("out", P),
+                ("ldo", I64), ("M", I64)]
+grp = sig("dc_w8a8_gemm_grouped", I, [P, I, I64, I64, I, I, P])
+gplan = sig("dc_w8a8_gemm_group_plan", I, [ctypes.POINTER(I64), I, I64, I64])
 BF16, F16, F32 = 1, 0, 2
+probs = (Prob * 4)(Prob(16, 512, 16, 512, 16, 16, None, 16, 3072, 64), Prob(16, 500, 16, 512, 16, 16, None, 16, 3072, 64),
+                   Prob(16, 512, None, 512, 16, 16, None, 16, 3072, 64), Prob(16, 512, 16, 512, 16, 16, None, 16, 3072, 0))
+Ms = (I64 * 4)(4096, 512, 0, 77)
 st = (I64 * 3)(8, 8, 8)
 bad = (I64 * 3)(8, 12, 8)
 checks = [
@@ -79,6 +87,14 @@ checks = [
     (anoa(16, 16, 16, 16, BF16, 8, 32, 8192, 8192, 128, st, st, st, st, 0.1, None), 4),
     (anoa(16, 16, 16, 16, BF16, 1, 1, 4, 4, 200, st, st, st, st, 0.1, None), 2),
     (qq(None, BF16, 1, 1, 4, 64, st, 16, 16, None), 1),
+    (grp(probs, 0, 3072, 512, -1, BF16, None), 1),
+    (grp(probs, 5, 3072, 512, -1, BF16, None), 1),
+    (grp(probs, 2, 3072, 320, -1, BF16, None), 2),
+    (grp(probs, 2, 3072, 512, -1, BF16, None), 2),
+    (grp(ctypes.byref(probs, 2 * ctypes.sizeof(Prob)), 2, 3072, 512, -1, BF16, None), 1),
+    (grp(ctypes.byref(probs, 3 * ctypes.sizeof(Prob)), 1, 3072, 512, -1, BF16, None), 0),
+    (gplan(Ms, 4, 3072, 3072), 1),
+    (gplan(Ms, 9, 3072, 3072), -1),
 ]
 for i, (rc, want) in enumerate(checks):
     if rc != want:

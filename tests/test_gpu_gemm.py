@@ -213,3 +213,72 @@ def test_split_k_is_bit_identical(gpu, mnk, dtype):
     assert torch.equal(split, _gemm_unsplit(q, w, sx, sw, bias, dtype))
     for _ in range(4):
         assert torch.equal(_int8._gemm(q, w, sx, sw, bias, dtype), split)
+
+
+# grouped launches (dc_w8a8_gemm_grouped): (row counts, N, K); M = 0 problems
+# are skipped, ragged M and N exercise the partial tiles
+GROUPS = [([4096, 512], 3072, 3072), ([1000, 77, 300], 1000, 512), ([257, 0, 513, 64], 640, 256),
+          ([512, 4096], 3072, 1024)]
+
+
+@pytest.mark.parametrize("ms,n,k", GROUPS)
+@pytest.mark.parametrize("dtype,bias_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, None),
+                                              (torch.float32, torch.float32), (torch.int32, None)])
+def test_grouped_gemm_equals_separate_calls(gpu, ms, n, k, dtype, bias_dtype):
+    """One grouped launch over problems with their own activations, weights,
+    scales and biases: every output bit-identical to dc_w8a8_gemm on that
+    problem alone (and the first one to the oracle)."""
+    items, seps = [], []
+    for i, m in enumerate(ms):
+        q, w, sx, sw = _qw(m, n, k, 40 + i)
+        b = (torch.randn(n, generator=torch.Generator().manual_seed(50 + i)) * 0.5).to(bias_dtype) \
+            if bias_dtype is not None else None
+        q, w, sx, sw = q.to(gpu), w.to(gpu), sx.to(gpu), sw.to(gpu)
+        b = b.to(gpu) if b is not None else None
+        items.append((q, w, sx, sw, b))
+        seps.append(_gemm_unsplit(q, w, sx, sw, b, dtype) if dtype != torch.int32 else _int8.int_mm(q, w))
+    outs = _int8._gemm_grouped(items, dtype)
+    for m, out, sep in zip(ms, outs, seps):
+        assert out.shape == (m, n) and out.dtype == dtype
+        assert torch.equal(out, sep)
+    q, w, sx, sw, b = (t.cpu() if t is not None else None for t in items[0])
+    acc = OG.int_mm(q.numpy(), w.numpy())
+    if dtype == torch.int32:
+        assert np.array_equal(outs[0].cpu().numpy(), acc)
+    else:
+        ref = OG.rescale(acc, sx.numpy(), sw.numpy(), np32(b) if b is not None else None, DT[dtype])
+        assert np.array_equal(np32(outs[0]).view(np.uint32), ref.view(np.uint32))
+
+
+def test_grouped_gemm_strided_rows(gpu):
+    """Row strides above K (a column slice of wider activations and weights)."""
+    k, n = 512, 384
+    a_wide = torch.randint(-127, 128, (700, 1024), dtype=torch.int8, device=gpu)
+    w_wide = torch.randint(-127, 128, (n, 768), dtype=torch.int8, device=gpu)
+    sx, sw = torch.rand(700, device=gpu) * 1e-2, torch.rand(n, device=gpu) * 1e-3
+    items = [(a_wide[:300, :k], w_wide[:, :k], sx[:300], sw, None), (a_wide[300:, 256:256 + k], w_wide[:, 128:128 + k],
+                                                                    sx[300:], sw, None)]
+    outs = _int8._gemm_grouped(items, torch.bfloat16)
+    for (q, w, x_s, w_s, _), out in zip(items, outs):
+        assert torch.equal(out, _gemm_unsplit(q.contiguous(), w.contiguous(), x_s.contiguous(), w_s, None,
+                                              torch.bfloat16))
+
+
+def test_group_plan_and_layers(gpu):
+    """The plan groups FLUX's double-block pairs whose 256 x 256 tiles add no
+    round (qkv, proj, MLP down on 256 CUs) and not MLP up; grouped W8A8 layers
+    equal the layers run one by one."""
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert _int8.gemm_group_plan([4096, 512], 9216, 3072)
+        assert _int8.gemm_group_plan([4096, 512], 3072, 3072)
+        assert _int8.gemm_group_plan([4096, 512], 3072, 12288)
+        assert not _int8.gemm_group_plan([4096, 512], 12288, 3072)
+    assert not _int8.gemm_group_plan([4096], 3072, 3072)
+    assert not _int8.gemm_group_plan([4096, 512], 3072, 3000)
+    torch.manual_seed(3)
+    la = _int8.Int8Linear.from_linear(nn.Linear(3072, 3072).to(gpu).to(torch.bfloat16), 256)
+    lb = _int8.Int8Linear.from_linear(nn.Linear(3072, 3072).to(gpu).to(torch.bfloat16), 256)
+    xa = torch.randn(2, 2048, 3072, device=gpu).to(torch.bfloat16)
+    xb = torch.randn(1, 512, 3072, device=gpu).to(torch.bfloat16)
+    ya, yb = _int8.linear_group([la, lb], [xa, xb])
+    assert torch.equal(ya, la(xa)) and torch.equal(yb, lb(xb))

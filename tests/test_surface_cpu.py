@@ -260,6 +260,35 @@ def test_argument_checks_fail_before_any_launch():
     assert b"ld2" in so.dc_last_error()
     assert so.dc_act_quantize_rows(None, 0, 0, 16, 512, 256, 4, _lib.F16, 4, 256, 16, 256, 16, None) == 1
     assert b"unknown act" in so.dc_last_error()
+    # dc_w8a8_gemm_grouped: counts, K, dtypes and each problem's pointers / strides
+    P = _lib.GemmProblem
+    probs = (P * 2)(P(16, 512, 16, 512, 16, 16, None, 16, 3072, 4096), P(16, 512, 16, 512, 16, 16, None, 16, 3072, 512))
+    assert so.dc_w8a8_gemm_grouped(probs, 0, 3072, 512, -1, _lib.BF16, None) == 1
+    assert so.dc_w8a8_gemm_grouped(probs, 5, 3072, 512, -1, _lib.BF16, None) == 1
+    assert so.dc_w8a8_gemm_grouped(None, 2, 3072, 512, -1, _lib.BF16, None) == 1
+    assert so.dc_w8a8_gemm_grouped(probs, 2, 3072, 320, -1, _lib.BF16, None) == 2 and b"256" in so.dc_last_error()
+    assert so.dc_w8a8_gemm_grouped(probs, 2, 3072, 512, 9, _lib.BF16, None) == 1 and b"bias" in so.dc_last_error()
+    assert so.dc_w8a8_gemm_grouped(probs, 2, 3072, 512, -1, 7, None) == 1 and b"out_dtype" in so.dc_last_error()
+    bad = (P * 2)(P(16, 512, 16, 512, 16, 16, None, 16, 3072, 64), P(16, 500, 16, 512, 16, 16, None, 16, 3072, 64))
+    assert so.dc_w8a8_gemm_grouped(bad, 2, 3072, 512, -1, _lib.BF16, None) == 2 and b"lda" in so.dc_last_error()
+    bad = (P * 2)(P(16, 512, 16, 512, 16, 16, None, 16, 3072, 64), P(16, 512, None, 512, 16, 16, None, 16, 3072, 64))
+    assert so.dc_w8a8_gemm_grouped(bad, 2, 3072, 512, -1, _lib.BF16, None) == 1 and b"null" in so.dc_last_error()
+    bad = (P * 1)(P(16, 512, 16, 512, 16, 16, None, 16, 3072, -1))
+    assert so.dc_w8a8_gemm_grouped(bad, 1, 3072, 512, -1, _lib.BF16, None) == 1 and b"negative" in so.dc_last_error()
+    bad = (P * 1)(P(16, 512, 16, 512, None, 16, None, 16, 3072, 8))
+    assert so.dc_w8a8_gemm_grouped(bad, 1, 3072, 512, -1, _lib.BF16, None) == 1 and b"scales" in so.dc_last_error()
+    bad = (P * 1)(P(16, 512, 16, 512, 16, 16, None, 16, 3000, 8))
+    assert so.dc_w8a8_gemm_grouped(bad, 1, 3072, 512, -1, _lib.BF16, None) == 1 and b"ldo" in so.dc_last_error()
+    empty = (P * 2)(P(16, 512, 16, 512, 16, 16, None, 16, 3072, 0), P(None, 0, None, 0, None, None, None, None, 0, 0))
+    assert so.dc_w8a8_gemm_grouped(empty, 2, 3072, 512, -1, _lib.BF16, None) == 0       # nothing to run
+    # the group plan (256 CUs when no device answers): FLUX's double-block pairs
+    Ms = (_lib.ctypes.c_int64 * 2)(4096, 512)
+    assert so.dc_w8a8_gemm_group_plan(Ms, 2, 9216, 3072) == 1          # 576 + 72 tiles: 3 rounds either way
+    assert so.dc_w8a8_gemm_group_plan(Ms, 2, 3072, 3072) == 1          # 192 + 24: 1 round
+    assert so.dc_w8a8_gemm_group_plan(Ms, 2, 12288, 3072) == 0         # 768 + 96: 4 rounds against 3
+    assert so.dc_w8a8_gemm_group_plan(Ms, 2, 3072, 3000) == 0          # K not a multiple of 256
+    assert so.dc_w8a8_gemm_group_plan(Ms, 1, 3072, 3072) == 0          # one problem
+    assert so.dc_w8a8_gemm_group_plan(Ms, 0, 3072, 3072) == -1
 
 
 def test_bench_refuses_more_than_one_gpu():
