@@ -7,7 +7,7 @@ captured input buffers must reach the next replay.
 
 Covered: the quantize kernel, each GEMM plan the FLUX step uses (DMA-fed
 256 x 256, 192 x 256 / 128 x 128, split-K with its workspace and epilogue
-pass) and the INT8 attention (K statistics, K quantize, attention): the
+pass, a grouped launch of two layers) and the INT8 attention (K statistics, K quantize, attention): the
 256-query kernel at the FLUX shape, stream-K pieces and their merge at SDXL's
 4096-token self-attention, and the 128-query kernel whole.
 """
@@ -23,8 +23,9 @@ from diffucore_amd import _int8, attention_bhld
 pytestmark = pytest.mark.gpu
 
 BF16 = torch.bfloat16
-# (M, K, N): DMA-fed 256 x 256 plan, split-K (M = 512, K = 3072), a ragged one
-LINEARS = [(4096, 512, 4096), (512, 3072, 3072), (1000, 768, 1280)]
+# (M, K, N): DMA-fed 256 x 256 plan, split-K (M = 512, K = 3072), a ragged one;
+# the last two run as one grouped launch (dc_w8a8_gemm_grouped)
+LINEARS = [(4096, 512, 4096), (512, 3072, 3072), (1000, 768, 1280), (1024, 512, 1024), (300, 512, 1024)]
 ATTN = [(1, 24, 4608, 128), (2, 10, 4096, 64), (1, 4, 1000, 64)]
 
 
@@ -38,7 +39,9 @@ def _case(gpu, seed):
 
 
 def _step(layers, xs, qkvs):
-    ys = [layer.matmul_quantized(*_int8.quantize_activation(x, layer.group), BF16) for layer, x in zip(layers, xs)]
+    ys = [layer.matmul_quantized(*_int8.quantize_activation(x, layer.group), BF16)
+          for layer, x in zip(layers[:3], xs[:3])]
+    ys += _int8.linear_group(layers[3:], xs[3:])
     return ys + [attention_bhld(q, k, v, "int8_turing") for q, k, v in qkvs]
 
 
@@ -46,6 +49,7 @@ def test_graph_replays_equal_eager_calls(gpu):
     layers, xs, qkvs = _case(gpu, 3)
     m, k, n = LINEARS[0]
     assert _int8.gemm_plan(m, n, k) == "dma_256x256"
+    assert _int8.gemm_group_plan([LINEARS[3][0], LINEARS[4][0]], LINEARS[3][2], LINEARS[3][1])
     with torch.no_grad():
         want = [t.clone() for t in _step(layers, xs, qkvs)]
         side = torch.cuda.Stream()
