@@ -7,6 +7,7 @@ raw device pointers and ``hipStream_t`` handles from torch are valid in it.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import functools
 from pathlib import Path
@@ -108,8 +109,24 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed (code {rc}): {msg}")
 
 
+# torch's raw current-stream query (the handle only, no Stream object: about
+# 0.1 us against 3 us per call); the public API where it is missing
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
+    """The ``hipStream_t`` of torch's current stream on ``device``."""
+    if _raw_stream is not None:
+        return _raw_stream(torch.cuda.current_device() if device.index is None else device.index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def device_ctx(device: torch.device):
+    """``torch.cuda.device(device)`` when ``device`` is not the current one,
+    else a no-op context (entering torch's costs about 3 us per call)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def strides3(t: torch.Tensor):

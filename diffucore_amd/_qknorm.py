@@ -104,7 +104,7 @@ def norm_rope(q: torch.Tensor, q_weight: torch.Tensor, eps: float, freqs: torch.
     def st(t):
         return _lib.strides3(t) if t is not None else None
 
-    with torch.cuda.device(q.device):
+    with _lib.device_ctx(q.device):
         rc = so.dc_qk_norm_rope(_lib.dtype_code(q.dtype), B, L, H, D, flags, ctypes.c_float(eps),
                                 ptr(q), st(q), ptr(q_weight), ptr(k), st(k), ptr(k_weight), _lib.dtype_code(wdt),
                                 ptr(freqs), fb, fl, ptr(oq), st(oq), ptr(ok_), st(ok_), ptr(v), st(v), ptr(ov),
