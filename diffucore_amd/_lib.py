@@ -123,15 +123,22 @@ def stream_ptr(device: torch.device) -> int:
 
 def device_ctx(device: torch.device):
     """``torch.cuda.device(device)`` when ``device`` is not the current one,
-    else a no-op context (entering torch's costs about 3 us per call)."""
+    else a no-op context (entering torch's costs about 3 us per call). A
+    device that is not a GPU raises: the kernels take device pointers only."""
+    if device.type != "cuda":
+        raise RuntimeError(f"diffucore_amd: the HIP kernels take GPU tensors (got a {device} tensor)")
     if device.index is None or device.index == torch.cuda.current_device():
         return contextlib.nullcontext()
     return torch.cuda.device(device)
 
 
+_I64X3 = ctypes.c_int64 * 3
+
+
 def strides3(t: torch.Tensor):
-    arr = (ctypes.c_int64 * 3)(*t.stride()[:3])
-    return arr
+    """The first three strides of ``t`` as a C ``int64_t[3]``."""
+    s = t.stride()
+    return _I64X3(s[0], s[1], s[2])
 
 
 @functools.cache

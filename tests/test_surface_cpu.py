@@ -179,6 +179,24 @@ def test_hot_path_has_no_cpu_fallback():
                        torch.ones(3), torch.ones(8), torch.float16) is None
 
 
+def test_entry_points_refuse_host_tensors_before_any_launch():
+    """Every wrapper that reaches the C ABI enters the device context first,
+    and that refuses a CPU device: host pointers never reach a kernel."""
+    from diffucore_amd import _attention as A
+    from diffucore_amd import _lib
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        _lib.device_ctx(torch.device("cpu"))
+    if _lib.lib() is None:
+        pytest.skip(f"library not built: {_lib.load_error()}")
+    q = torch.randn(1, 200, 2, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        A.int8_attention(q, q, q, 0.125)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        A.quantize_q(q)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        D.rescale(torch.zeros(3, 8, dtype=torch.int32), torch.ones(3), torch.ones(8), None, torch.float16)
+
+
 def test_quantize_and_dequantize_linears():
     model = nn.Sequential(nn.Linear(512, 256), nn.GELU(), nn.Linear(256, 64))
     assert D.quantize_linears(model, ["0", "2"], "cpu", group=0) == 2
