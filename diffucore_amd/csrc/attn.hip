@@ -789,7 +789,7 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs p) {
 // Measured on MI355X (FLUX shape): the kernel is bound by its instruction
 // stream, not by memory or synchronization. With the loads and barriers
 // removed it runs within 12% of its full time, and MFMA (31% busy) and VALU
-// (41% busy) work barely overlap on a SIMD: a microbenchmark of one tile's
+// (34% busy) work barely overlap on a SIMD: a microbenchmark of one tile's
 // mix (24 MFMAs, ~100 softmax VALU instructions) runs at about the sum of
 // the two alone however it is arranged.
 constexpr int BQW = 256;                            // query rows per workgroup
