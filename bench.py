@@ -648,7 +648,8 @@ def main():
             "latent_cos_vs_bf16": round(float(a @ b / (a.norm() * b.norm())), 6),
             "what": "full synthetic FLUX.1-schnell forward + euler update at 1024^2 (flux_step.py), "
                     "4-step final latent compared; int8 = W8A8 linears + INT8 attention + fused glue "
-                    "(LayerNorm-modulate/GELU quantize passes, QK norm + rotary); bf16 = the reference's "
+                    "(LayerNorm-modulate/GELU quantize passes, QK norm + rotary, gate + residual in the GEMM "
+                    "epilogue); bf16 = the reference's "
                     "eager ops, bf16_fused_glue = bf16 with only the QK norm + rotary pass fused",
         }
         log(f"full step: int8 {int8_ms:.2f} ms vs bf16 {bf16_ms:.2f} ms")

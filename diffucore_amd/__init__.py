@@ -7,7 +7,8 @@ from ._attention import (attention_bhld, attention_blhd, fa2_turing_available, i
 from ._int8 import (GROUP, Int8Embedding, Int8Linear, act_quantize, adopt_int8_embedding, adopt_int8_layers,
                     dequantize_linears, dequantize_weight, fuse_linears, geglu_quantize, gelu_quantize,
                     int8_fast_available, int8_geglu_ff,
-                    int8_layers, int8_mlp, int_mm, linear_group, ln_mod_quantize, matmul_quantized_group, lora_seed, quantize_activation,
+                    int8_layers, int8_mlp, int_mm, linear_group, ln_mod_quantize, matmul_quantized_gated,
+                    matmul_quantized_group, lora_seed, quantize_activation,
                     quantize_linears, quantize_weight, rescale, scaled_mm, shared_qkv)
 from ._qknorm import flux_qk_norm_rope, norm_rope, qk_norm_rope, qk_ok, set_fused_glue
 from .runtime import DevicePolicy
@@ -18,7 +19,7 @@ __all__ = sorted([
     "fa2_turing_available", "flux_qk_norm_rope", "fuse_linears", "geglu_quantize", "gelu_quantize",
     "int8_attention", "int8_geglu_ff",
     "int8_fast_available", "int8_layers", "int8_mlp", "int8_turing_available", "int_mm", "linear_group",
-    "ln_mod_quantize", "matmul_quantized_group",
+    "ln_mod_quantize", "matmul_quantized_gated", "matmul_quantized_group",
     "lora_seed", "norm_rope", "qk_norm_rope", "qk_ok", "quantize_activation", "quantize_linears",
     "quantize_weight", "rescale", "resolve_attention_backend", "scaled_mm", "set_attention_backend",
     "set_fused_glue", "shared_qkv",

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libdiffucore_amd.so"
 
 F16, BF16, F32, I32, NONE = 0, 1, 2, 3, -1
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _DTYPE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int32: I32}
 
@@ -32,6 +32,7 @@ _SIGS = {
     "dc_w8a8_gemm_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
     "dc_w8a8_gemm_plan": (_I, [_I64, _I64, _I64, _I64, _I64]),
     "dc_w8a8_gemm_grouped": (_I, [_P, _I, _I64, _I64, _I, _I, _P]),
+    "dc_w8a8_gemm_grouped_gated": (_I, [_P, _P, _I, _I64, _I64, _I, _I, _P]),
     "dc_w8a8_gemm_group_plan": (_I, [ctypes.POINTER(_I64), _I, _I64, _I64]),
     "dc_rescale": (_I, [_P, _I64, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P]),
     "dc_ln_mod_quantize_rows": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, ctypes.c_float, _I, _P, _I64, _P, _P]),
@@ -59,6 +60,12 @@ class GemmProblem(ctypes.Structure):
     """``dc_gemm_problem``: one problem of ``dc_w8a8_gemm_grouped``."""
     _fields_ = [("a", _P), ("lda", _I64), ("w", _P), ("ldw", _I64), ("sx", _P), ("sw", _P), ("bias", _P),
                 ("out", _P), ("ldo", _I64), ("M", _I64)]
+
+
+class GemmGate(ctypes.Structure):
+    """``dc_gemm_gate``: one problem's residual and gate for
+    ``dc_w8a8_gemm_grouped_gated``."""
+    _fields_ = [("res", _P), ("ldr", _I64), ("gate", _P)]
 
 _load_error = ""
 

@@ -46,6 +46,12 @@ struct GemmArgs {
   // and writes its partial sums at out + y * split_stride
   int ksplit, kslice;
   int64_t split_stride;
+  // gated residual (dc_w8a8_gemm_grouped_gated; DMA-fed kernel only):
+  // out = res + gate * y, res [M, N] with row stride ldr, gate [N], both of
+  // the output dtype
+  const void* res;
+  const void* gate;
+  int64_t ldr;
 };
 
 // One problem of a grouped launch (dc_w8a8_gemm_grouped): the per-problem
@@ -59,6 +65,9 @@ struct GroupProblem {
   void* out;
   int64_t lda, ldw, ldo;
   int M, tiles_m, vec_out, vec16;
+  const void* res;
+  const void* gate;
+  int64_t ldr;
 };
 
 // A grouped launch of the DMA-fed kernel: problem g owns logical tiles
@@ -122,6 +131,35 @@ __device__ __forceinline__ uint32_t epi_pair(int a0, int a1, float sxm, float s0
   return pk;
 }
 
+// Gated residual on an output y (FLUX's x + gate * y, rounded as torch
+// rounds its two ops): t = round(gate * y), out = round(res + t), each to the
+// output type, with no contraction into an FMA.
+template <int OUT_DT>
+__device__ __forceinline__ float gated1(float y, float r, float g) {
+  return round_to<OUT_DT>(materialize(r + round_to<OUT_DT>(materialize(g * y))));
+}
+// The same on two packed 16-bit outputs / residuals (one packed conversion
+// per rounding step).
+template <int OUT_DT>
+__device__ __forceinline__ uint32_t gated_pair(uint32_t y2, uint32_t r2, float g0, float g1) {
+  const uint32_t t2 = cvt_pair<OUT_DT>(materialize(g0 * pair_lo<OUT_DT>(y2)), materialize(g1 * pair_hi<OUT_DT>(y2)));
+  return cvt_pair<OUT_DT>(materialize(pair_lo<OUT_DT>(r2) + pair_lo<OUT_DT>(t2)),
+                          materialize(pair_hi<OUT_DT>(r2) + pair_hi<OUT_DT>(t2)));
+}
+// Eight packed 16-bit outputs (or four float32 ones) of one 16-byte chunk.
+template <int OUT_DT>
+__device__ __forceinline__ uint4 gated_chunk(uint4 y, uint4 r, const float* g) {
+  if constexpr (OUT_DT == DC_F32) {
+    return make_uint4(__float_as_uint(gated1<OUT_DT>(__uint_as_float(y.x), __uint_as_float(r.x), g[0])),
+                      __float_as_uint(gated1<OUT_DT>(__uint_as_float(y.y), __uint_as_float(r.y), g[1])),
+                      __float_as_uint(gated1<OUT_DT>(__uint_as_float(y.z), __uint_as_float(r.z), g[2])),
+                      __float_as_uint(gated1<OUT_DT>(__uint_as_float(y.w), __uint_as_float(r.w), g[3])));
+  } else {
+    return make_uint4(gated_pair<OUT_DT>(y.x, r.x, g[0], g[1]), gated_pair<OUT_DT>(y.y, r.y, g[2], g[3]),
+                      gated_pair<OUT_DT>(y.z, r.z, g[4], g[5]), gated_pair<OUT_DT>(y.w, r.w, g[6], g[7]));
+  }
+}
+
 template <int OUT_DT>
 __device__ __forceinline__ void store1(void* out, int64_t idx, float y) {
   if constexpr (OUT_DT == DC_F32) static_cast<float*>(out)[idx] = y;
@@ -176,6 +214,7 @@ __device__ __forceinline__ void group_origin(GemmArgs& p, const GroupArgs& g, in
   p.a = DC_SEL(a); p.w = DC_SEL(w); p.sx = DC_SEL(sx); p.sw = DC_SEL(sw); p.bias = DC_SEL(bias);
   p.out = DC_SEL(out); p.lda = DC_SEL(lda); p.ldw = DC_SEL(ldw); p.ldo = DC_SEL(ldo);
   p.M = DC_SEL(M); p.tiles_m = DC_SEL(tiles_m); p.vec_out = DC_SEL(vec_out); p.vec16 = DC_SEL(vec16);
+  p.res = DC_SEL(res); p.gate = DC_SEL(gate); p.ldr = DC_SEL(ldr);
   const int first = k == 0 ? g.first[0] : k == 1 ? g.first[1] : k == 2 ? g.first[2] : g.first[3];
 #undef DC_SEL
   tile_coords(logical - first, p.tiles_m, p.tiles_n, BM, BN, m0, n0);
@@ -186,10 +225,11 @@ __device__ __forceinline__ void group_origin(GemmArgs& p, const GroupArgs& g, in
 // m = m0 + mb + 32 j + l32. sw_l / b_l / sx_l are the tile's channel scales,
 // rounded biases and row scales in LDS; each lane reads its row scales once
 // and each group of 4 channel scales / biases once for all its rows.
-template <int OUT_DT, int BIAS_DT, int FN, int FM>
+// RES: the gated residual, with the tile's gate values in g_l (LDS).
+template <int OUT_DT, int BIAS_DT, int FN, int FM, bool RES = false>
 __device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const GemmArgs& p, int m0, int n0, int nb,
                                            int mb, int BM, int BN, const float* sw_l, const float* b_l,
-                                           const float* sx_l, int hf, int l32) {
+                                           const float* sx_l, int hf, int l32, const float* g_l = nullptr) {
   constexpr bool HB = BIAS_DT != DC_NONE;
   const bool full = p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N;
   float sxm[FM];
@@ -202,12 +242,15 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const Gemm
       const int nl = nb + 32 * i + 8 * g + 4 * hf, n = n0 + nl;
       const bool vec = full || (p.vec_out && n + 3 < p.N);
       float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 g4 = make_float4(0.f, 0.f, 0.f, 0.f);
       if constexpr (OUT_DT != DC_I32) s4 = *reinterpret_cast<const float4*>(sw_l + nl);
       if constexpr (HB) b4 = *reinterpret_cast<const float4*>(b_l + nl);
+      if constexpr (RES) g4 = *reinterpret_cast<const float4*>(g_l + nl);
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
         const int m = m0 + mb + 32 * j + l32;
         if (!full && m >= p.M) continue;
+        const int64_t rbase = RES ? (int64_t)m * p.ldr + n : 0;
         const int64_t base = (int64_t)m * p.ldo + n;
         const int av[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
         if constexpr (OUT_DT == DC_I32) {
@@ -215,10 +258,26 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const Gemm
           if (vec) *reinterpret_cast<int4*>(o + base) = make_int4(av[0], av[1], av[2], av[3]);
           else for (int e = 0; e < 4 && n + e < p.N; ++e) o[base + e] = av[e];
         } else if constexpr (OUT_DT == DC_F32) {
-          const float y0 = epi_pre<OUT_DT, HB>(av[0], sxm[j], s4.x, b4.x);
-          const float y1 = epi_pre<OUT_DT, HB>(av[1], sxm[j], s4.y, b4.y);
-          const float y2 = epi_pre<OUT_DT, HB>(av[2], sxm[j], s4.z, b4.z);
-          const float y3 = epi_pre<OUT_DT, HB>(av[3], sxm[j], s4.w, b4.w);
+          float y0 = epi_pre<OUT_DT, HB>(av[0], sxm[j], s4.x, b4.x);
+          float y1 = epi_pre<OUT_DT, HB>(av[1], sxm[j], s4.y, b4.y);
+          float y2 = epi_pre<OUT_DT, HB>(av[2], sxm[j], s4.z, b4.z);
+          float y3 = epi_pre<OUT_DT, HB>(av[3], sxm[j], s4.w, b4.w);
+          if constexpr (RES) {
+            const float* r32 = static_cast<const float*>(p.res) + rbase;
+            float4 r4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (vec) {
+              r4 = *reinterpret_cast<const float4*>(r32);
+            } else {
+              if (n < p.N) r4.x = r32[0];
+              if (n + 1 < p.N) r4.y = r32[1];
+              if (n + 2 < p.N) r4.z = r32[2];
+              if (n + 3 < p.N) r4.w = r32[3];
+            }
+            y0 = gated1<OUT_DT>(y0, r4.x, g4.x);
+            y1 = gated1<OUT_DT>(y1, r4.y, g4.y);
+            y2 = gated1<OUT_DT>(y2, r4.z, g4.z);
+            y3 = gated1<OUT_DT>(y3, r4.w, g4.w);
+          }
           if (vec) {
             *reinterpret_cast<float4*>(static_cast<float*>(p.out) + base) = make_float4(y0, y1, y2, y3);
           } else {
@@ -226,8 +285,22 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const Gemm
             for (int e = 0; e < 4 && n + e < p.N; ++e) store1<OUT_DT>(p.out, base + e, yv[e]);
           }
         } else {
-          const uint32_t lo = epi_pair<OUT_DT, HB>(av[0], av[1], sxm[j], s4.x, s4.y, b4.x, b4.y);
-          const uint32_t hi = epi_pair<OUT_DT, HB>(av[2], av[3], sxm[j], s4.z, s4.w, b4.z, b4.w);
+          uint32_t lo = epi_pair<OUT_DT, HB>(av[0], av[1], sxm[j], s4.x, s4.y, b4.x, b4.y);
+          uint32_t hi = epi_pair<OUT_DT, HB>(av[2], av[3], sxm[j], s4.z, s4.w, b4.z, b4.w);
+          if constexpr (RES) {
+            const uint16_t* r16 = static_cast<const uint16_t*>(p.res) + rbase;
+            uint32_t rlo, rhi;
+            if (vec) {
+              const uint2 rr = *reinterpret_cast<const uint2*>(r16);
+              rlo = rr.x, rhi = rr.y;
+            } else {
+              uint32_t rv[4] = {0u, 0u, 0u, 0u};
+              for (int e = 0; e < 4 && n + e < p.N; ++e) rv[e] = r16[e];
+              rlo = rv[0] | (rv[1] << 16), rhi = rv[2] | (rv[3] << 16);
+            }
+            lo = gated_pair<OUT_DT>(lo, rlo, g4.x, g4.y);
+            hi = gated_pair<OUT_DT>(hi, rhi, g4.z, g4.w);
+          }
           uint16_t* o16 = static_cast<uint16_t*>(p.out);
           if (vec) {
             *reinterpret_cast<uint2*>(o16 + base) = make_uint2(lo, hi);
@@ -240,16 +313,19 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const Gemm
     }
 }
 
-// This tile's output-channel scales, biases (rounded to the output dtype) and
-// row scales into LDS for the epilogue (threads t = 0 .. nt - 1).
-template <int OUT_DT, int BIAS_DT>
+// This tile's output-channel scales, biases (rounded to the output dtype),
+// gate values (RES) and row scales into LDS for the epilogue (threads
+// t = 0 .. nt - 1).
+template <int OUT_DT, int BIAS_DT, bool RES = false>
 __device__ __forceinline__ void stage_epilogue_vectors(const GemmArgs& p, int m0, int n0, int BM, int BN, int t,
-                                                       int nt, float* sw_l, float* b_l, float* sx_l) {
+                                                       int nt, float* sw_l, float* b_l, float* sx_l,
+                                                       float* g_l = nullptr) {
   if constexpr (OUT_DT != DC_I32) {
     for (int i = t; i < BN; i += nt) {
       const int n = min(n0 + i, p.N - 1);
       sw_l[i] = p.sw[n];
       if constexpr (BIAS_DT != DC_NONE) b_l[i] = round_to<OUT_DT>(load_bias<BIAS_DT>(p.bias, n));
+      if constexpr (RES) g_l[i] = load_bias<OUT_DT>(p.gate, n);   // the gate is of the output dtype
     }
     for (int i = t; i < BM; i += nt) sx_l[i] = p.sx[min(m0 + i, p.M - 1)];
   }
@@ -264,21 +340,42 @@ __device__ __forceinline__ void stage_epilogue_vectors(const GemmArgs& p, int m0
 // instruction. 32-bit outputs take two passes of 64 rows. A lane reads back
 // what other lanes of its wave wrote: the wavefront fences and barrier
 // between the two halves keep the compiler from moving LDS accesses across.
-template <int OUT_DT, int BIAS_DT>
+// RES: the gated residual. The residual chunks the lane stores go through a
+// ring of RRING registers, loaded RRING stores ahead: the first RRING before
+// the pass converts (they land meanwhile), each later one as its slot frees
+// (a whole pass at once would spill). The lane's gate values come from g_l.
+template <int OUT_DT, int BIAS_DT, bool RES = false>
 __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], const GemmArgs& p, int m0, int n0, int nb,
                                                int mb, const float* sw_l, const float* b_l, const float* sx_l, int hf,
-                                               int l32, int lane, uint8_t* stage) {
+                                               int l32, int lane, uint8_t* stage, const float* g_l = nullptr) {
   constexpr int OB = (OUT_DT == DC_F16 || OUT_DT == DC_BF16) ? 2 : 4;
   constexpr int ROWB = 128 * OB;   // staged row bytes
   constexpr int CH = ROWB / 16;    // 16-byte chunks per row
   constexpr int JP = 8 / OB;       // 32-row m blocks per pass
   constexpr int RPI = 64 / CH;     // rows per store instruction
+  constexpr int NIT = 32 * JP / RPI;   // store instructions per pass
+  constexpr int RRING = 8;             // residual chunks in flight per lane
   constexpr bool HB = BIAS_DT != DC_NONE;
+  const int c = lane % CH;
   float sxm[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) sxm[j] = OUT_DT != DC_I32 ? sx_l[mb + 32 * j + l32] : 0.0f;
+  float gv[RES ? 16 / OB : 1];
+  if constexpr (RES) {
+#pragma unroll
+    for (int e = 0; e < 16 / OB; ++e) gv[e] = g_l[nb + (16 / OB) * c + e];
+  }
 #pragma unroll
   for (int j0 = 0; j0 < 4; j0 += JP) {
+    uint4 rres[RES ? RRING : 1];
+    const uint8_t* rrow = RES ? static_cast<const uint8_t*>(p.res) + (n0 + nb) * OB + 16 * c : nullptr;
+    auto rload = [&](int k) __attribute__((always_inline)) {
+      return *reinterpret_cast<const uint4*>(rrow + (int64_t)(m0 + mb + 32 * j0 + RPI * k + lane / CH) * p.ldr * OB);
+    };
+    if constexpr (RES) {
+#pragma unroll
+      for (int k = 0; k < RRING; ++k) rres[k] = rload(k);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -313,11 +410,15 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], const Ge
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int c = lane % CH;
 #pragma unroll
-    for (int k = 0; k < 32 * JP / RPI; ++k) {
+    for (int k = 0; k < NIT; ++k) {
       const int r = RPI * k + lane / CH;
-      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * ROWB + 16 * (c ^ (r & 15)));
+      uint4 v = *reinterpret_cast<const uint4*>(stage + r * ROWB + 16 * (c ^ (r & 15)));
+      if constexpr (RES) {
+        const uint4 rk = rres[k % RRING];
+        if (k + RRING < NIT) rres[k % RRING] = rload(k + RRING);
+        v = gated_chunk<OUT_DT>(v, rk, gv);
+      }
       const int64_t m = m0 + mb + 32 * j0 + r;
       uint8_t* dst = static_cast<uint8_t*>(p.out) + (m * p.ldo + n0 + nb) * OB + 16 * c;
       *reinterpret_cast<uint4*>(dst) = v;
@@ -529,14 +630,15 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 #define DC_WAIT_VMCNT(n_) __builtin_amdgcn_s_waitcnt(((n_) & 15) | (((n_) >> 4) << 14) | (7 << 4) | (15 << 8))
 #define DC_WAIT_VMCNT_LGKM0(n_) __builtin_amdgcn_s_waitcnt(((n_) & 15) | (((n_) >> 4) << 14) | (7 << 4))
 
-template <int OUT_DT, int BIAS_DT>
+// RES: with the gated residual of dc_w8a8_gemm_grouped_gated.
+template <int OUT_DT, int BIAS_DT, bool RES = false>
 __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p, GroupArgs g) {
   constexpr int BN = 256, BM = 256, FN = 4, FM = 4;
   __shared__ __attribute__((aligned(1024))) uint8_t st0[DSTAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[DSTAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[DSTAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st3[DSTAGE];
-  __shared__ __attribute__((aligned(16))) float epi_v[2 * BN + BM];
+  __shared__ __attribute__((aligned(16))) float epi_v[(RES ? 3 : 2) * BN + BM];
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int l32 = lane & 31, hf = lane >> 5;
@@ -548,7 +650,8 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p, Group
   float* sw_l = epi_v;
   float* b_l = epi_v + BN;
   float* sx_l = epi_v + 2 * BN;
-  stage_epilogue_vectors<OUT_DT, BIAS_DT>(p, m0, n0, BM, BN, t, 256, sw_l, b_l, sx_l);
+  float* g_l = RES ? epi_v + 2 * BN + BM : nullptr;
+  stage_epilogue_vectors<OUT_DT, BIAS_DT, RES>(p, m0, n0, BM, BN, t, 256, sw_l, b_l, sx_l, g_l);
   __syncthreads();
 
   // DMA sources: wave w loads 1 KB blocks j = w + 4 u (rows 16 j .. 16 j + 15)
@@ -660,9 +763,11 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p, Group
   if (p.vec16 && m0 + BM <= p.M && n0 + BN <= p.N) {
     __syncthreads();   // every wave is done reading the stage buffers
     uint8_t* stg = w == 0 ? st0 : (w == 1 ? st1 : (w == 2 ? st2 : st3));
-    store_tile_lds<OUT_DT, BIAS_DT>(acc, p, m0, n0, wn * 128, wm * 128, sw_l, b_l, sx_l, hf, l32, lane, stg);
+    store_tile_lds<OUT_DT, BIAS_DT, RES>(acc, p, m0, n0, wn * 128, wm * 128, sw_l, b_l, sx_l, hf, l32, lane, stg,
+                                         g_l);
   } else {
-    store_tile<OUT_DT, BIAS_DT, FN, FM>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l, hf, l32);
+    store_tile<OUT_DT, BIAS_DT, FN, FM, RES>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l,
+                                             hf, l32, g_l);
   }
 }
 
@@ -762,10 +867,10 @@ static int launch_gemm_dma(GemmArgs p, hipStream_t st) {
 }
 
 // Grouped launch: g.first[g.ngroup] tiles in all (p holds N, K, tiles_n).
-template <int OUT_DT, int BIAS_DT>
+template <int OUT_DT, int BIAS_DT, bool RES = false>
 static int launch_gemm_dma_group(GemmArgs p, const GroupArgs& g, hipStream_t st) {
-  hipLaunchKernelGGL((w8a8_gemm_dma_kernel<OUT_DT, BIAS_DT>), dim3((unsigned)g.first[g.ngroup]), dim3(256), 0, st, p,
-                     g);
+  hipLaunchKernelGGL((w8a8_gemm_dma_kernel<OUT_DT, BIAS_DT, RES>), dim3((unsigned)g.first[g.ngroup]), dim3(256), 0, st,
+                     p, g);
   return launch_status("w8a8_gemm_dma_kernel");
 }
 
@@ -967,13 +1072,13 @@ extern "C" int dc_w8a8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
 
 // ---------------------------------------------------------------- grouped launches
 
-template <int OUT_DT>
+template <int OUT_DT, bool RES = false>
 static int group_bias(GemmArgs p, const GroupArgs& g, int bias_dtype, hipStream_t st) {
   switch (bias_dtype) {
-    case DC_NONE: return launch_gemm_dma_group<OUT_DT, DC_NONE>(p, g, st);
-    case DC_F16: return launch_gemm_dma_group<OUT_DT, DC_F16>(p, g, st);
-    case DC_BF16: return launch_gemm_dma_group<OUT_DT, DC_BF16>(p, g, st);
-    default: return launch_gemm_dma_group<OUT_DT, DC_F32>(p, g, st);
+    case DC_NONE: return launch_gemm_dma_group<OUT_DT, DC_NONE, RES>(p, g, st);
+    case DC_F16: return launch_gemm_dma_group<OUT_DT, DC_F16, RES>(p, g, st);
+    case DC_BF16: return launch_gemm_dma_group<OUT_DT, DC_BF16, RES>(p, g, st);
+    default: return launch_gemm_dma_group<OUT_DT, DC_F32, RES>(p, g, st);
   }
 }
 
@@ -1003,40 +1108,46 @@ extern "C" int dc_w8a8_gemm_group_plan(const int64_t* Ms, int count, int64_t N, 
   return (total + cus - 1) / cus <= (largest + cus - 1) / cus ? 1 : 0;
 }
 
-extern "C" int dc_w8a8_gemm_grouped(const dc_gemm_problem* problems, int count, int64_t N, int64_t K, int bias_dtype,
-                                    int out_dtype, void* stream) {
-  clear_error();
-  if (!problems) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: null pointer");
-  if (count < 1 || count > DC_GEMM_MAX_GROUP)
-    return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: count must be 1 .. DC_GEMM_MAX_GROUP");
-  if (N <= 0 || K <= 0) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: N and K must be positive");
-  if (N > 0x7fffffff || K > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: size too large");
-  if (K % (4 * DBK)) return fail(DC_EUNSUPPORTED, "dc_w8a8_gemm_grouped: needs K % 256 == 0");
+static int group_fail(int code, const char* who, const char* msg) {
+  set_error("%s: %s", who, msg);
+  return code;
+}
+
+// Checks and per-problem set-up shared by the grouped entry points. gates:
+// NULL, or one dc_gemm_gate per problem (the gated residual). An error
+// message starts with `who`.
+static int group_setup(const char* who, const dc_gemm_problem* problems, const dc_gemm_gate* gates, int count,
+                       int64_t N, int64_t K, int bias_dtype, int out_dtype, GemmArgs& p, GroupArgs& g) {
+  if (!problems) return group_fail(DC_EINVAL, who, "null pointer");
+  if (count < 1 || count > DC_GEMM_MAX_GROUP) return group_fail(DC_EINVAL, who, "count must be 1 .. DC_GEMM_MAX_GROUP");
+  if (N <= 0 || K <= 0) return group_fail(DC_EINVAL, who, "N and K must be positive");
+  if (N > 0x7fffffff || K > 0x7fffffff) return group_fail(DC_EINVAL, who, "size too large");
+  if (K % (4 * DBK)) return group_fail(DC_EUNSUPPORTED, who, "needs K % 256 == 0");
   if (out_dtype != DC_I32 && out_dtype != DC_F16 && out_dtype != DC_BF16 && out_dtype != DC_F32)
-    return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: bad out_dtype");
+    return group_fail(DC_EINVAL, who, "bad out_dtype");
   if (bias_dtype != DC_NONE && bias_dtype != DC_F16 && bias_dtype != DC_BF16 && bias_dtype != DC_F32)
-    return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: bad bias_dtype");
+    return group_fail(DC_EINVAL, who, "bad bias_dtype");
   const int ob = elem_bytes(out_dtype);
-  GemmArgs p{};
+  p = GemmArgs{};
   p.N = (int)N;
   p.K = (int)K;
   p.tiles_n = (int)((N + 255) / 256);
-  GroupArgs g{};
+  g = GroupArgs{};
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i) {
     const dc_gemm_problem& q = problems[i];
-    if (q.M < 0) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: negative M");
+    if (q.M < 0) return group_fail(DC_EINVAL, who, "negative M");
     if (q.M == 0) continue;
-    if (q.M > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: size too large");
-    if (!q.a || !q.w || !q.out) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: null pointer");
+    if (q.M > 0x7fffffff) return group_fail(DC_EINVAL, who, "size too large");
+    if (!q.a || !q.w || !q.out) return group_fail(DC_EINVAL, who, "null pointer");
     if (q.lda < K || q.ldw < K || q.lda % 16 || q.ldw % 16 || !aligned16(q.a) || !aligned16(q.w) ||
         256 * q.lda >= (int64_t(1) << 31) || 256 * q.ldw >= (int64_t(1) << 31))
-      return fail(DC_EUNSUPPORTED,
-                  "dc_w8a8_gemm_grouped: needs lda, ldw >= K, multiples of 16 and below 2^23, 16-byte aligned a, w");
-    if (q.ldo < N) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: ldo < N");
-    if (out_dtype != DC_I32 && (!q.sx || !q.sw)) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: scales are required");
+      return group_fail(DC_EUNSUPPORTED, who,
+                        "needs lda, ldw >= K, multiples of 16 and below 2^23, 16-byte aligned a, w");
+    if (q.ldo < N) return group_fail(DC_EINVAL, who, "ldo < N");
+    if (out_dtype != DC_I32 && (!q.sx || !q.sw)) return group_fail(DC_EINVAL, who, "scales are required");
     if (bias_dtype != DC_NONE && out_dtype != DC_I32 && !q.bias)
-      return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: bias_dtype given without bias");
+      return group_fail(DC_EINVAL, who, "bias_dtype given without bias");
     GroupProblem& d = g.prob[g.ngroup];
     d.a = q.a; d.w = q.w; d.sx = q.sx; d.sw = q.sw; d.bias = q.bias; d.out = q.out;
     d.lda = q.lda; d.ldw = q.ldw; d.ldo = q.ldo;
@@ -1045,19 +1156,57 @@ extern "C" int dc_w8a8_gemm_grouped(const dc_gemm_problem* problems, int count, 
     d.vec_out = ((reinterpret_cast<uintptr_t>(q.out) % (4 * (uintptr_t)ob)) == 0) && (q.ldo % 4 == 0) &&
                 (out_dtype == DC_I32 || (reinterpret_cast<uintptr_t>(q.sw) & 15) == 0);
     d.vec16 = d.vec_out && (reinterpret_cast<uintptr_t>(q.out) % 16) == 0 && (q.ldo * ob) % 16 == 0;
+    if (gates) {
+      const dc_gemm_gate& r = gates[i];
+      if (!r.res || !r.gate) return group_fail(DC_EINVAL, who, "null residual or gate");
+      if (r.ldr < N) return group_fail(DC_EINVAL, who, "ldr < N");
+      d.res = r.res; d.gate = r.gate; d.ldr = r.ldr;
+      // the residual's loads follow the output's stores, so they need the same alignment
+      d.vec_out = d.vec_out && (reinterpret_cast<uintptr_t>(r.res) % (4 * (uintptr_t)ob)) == 0 && r.ldr % 4 == 0;
+      d.vec16 = d.vec16 && d.vec_out && (reinterpret_cast<uintptr_t>(r.res) % 16) == 0 && (r.ldr * ob) % 16 == 0;
+    }
     g.first[g.ngroup] = (int)tiles;
     tiles += (int64_t)d.tiles_m * p.tiles_n;
-    if (tiles > 0x7fffffff) return fail(DC_EINVAL, "dc_w8a8_gemm_grouped: problem too large");
+    if (tiles > 0x7fffffff) return group_fail(DC_EINVAL, who, "problem too large");
     ++g.ngroup;
   }
-  if (g.ngroup == 0) return DC_OK;
   g.first[g.ngroup] = (int)tiles;
+  return DC_OK;
+}
+
+extern "C" int dc_w8a8_gemm_grouped(const dc_gemm_problem* problems, int count, int64_t N, int64_t K, int bias_dtype,
+                                    int out_dtype, void* stream) {
+  clear_error();
+  GemmArgs p;
+  GroupArgs g;
+  if (int e = group_setup("dc_w8a8_gemm_grouped", problems, nullptr, count, N, K, bias_dtype, out_dtype, p, g))
+    return e;
+  if (g.ngroup == 0) return DC_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (out_dtype) {
     case DC_I32: return launch_gemm_dma_group<DC_I32, DC_NONE>(p, g, st);
     case DC_F16: return group_bias<DC_F16>(p, g, bias_dtype, st);
     case DC_BF16: return group_bias<DC_BF16>(p, g, bias_dtype, st);
     default: return group_bias<DC_F32>(p, g, bias_dtype, st);
+  }
+}
+
+extern "C" int dc_w8a8_gemm_grouped_gated(const dc_gemm_problem* problems, const dc_gemm_gate* gates, int count,
+                                          int64_t N, int64_t K, int bias_dtype, int out_dtype, void* stream) {
+  clear_error();
+  const char* who = "dc_w8a8_gemm_grouped_gated";
+  if (!gates) return group_fail(DC_EINVAL, who, "null pointer");
+  if (out_dtype != DC_F16 && out_dtype != DC_BF16 && out_dtype != DC_F32)
+    return group_fail(DC_EINVAL, who, "out_dtype must be DC_F16, DC_BF16 or DC_F32");
+  GemmArgs p;
+  GroupArgs g;
+  if (int e = group_setup(who, problems, gates, count, N, K, bias_dtype, out_dtype, p, g)) return e;
+  if (g.ngroup == 0) return DC_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case DC_F16: return group_bias<DC_F16, true>(p, g, bias_dtype, st);
+    case DC_BF16: return group_bias<DC_BF16, true>(p, g, bias_dtype, st);
+    default: return group_bias<DC_F32, true>(p, g, bias_dtype, st);
   }
 }
 

@@ -211,6 +211,29 @@ int dc_w8a8_gemm_grouped(const dc_gemm_problem* problems, int count, int64_t N, 
                          int out_dtype, void* stream);
 
 /*
+ * dc_w8a8_gemm_grouped with a gated residual in the epilogue: problem i's
+ * output is res + gate * y, y being what dc_w8a8_gemm_grouped writes (scales,
+ * bias, cast), rounded as torch rounds FLUX's two bf16 ops: t = round(gate[n]
+ * * y[m, n]), out[m, n] = round(res[m, n] + t), each to out_dtype (DC_F16,
+ * DC_BF16 or DC_F32), with no fused multiply-add. No counterpart in the
+ * reference, whose FLUX blocks run the linear, then x + gate * out as two
+ * torch ops (flux_dit.py:298-301, 336); it is for callers that apply such
+ * a gate and residual to a W8A8 layer's output (FLUX's attention projection,
+ * MLP down and single-block linear2), saving those two passes over [M, N].
+ * gates[i].res is [M, N] of out_dtype with row stride ldr >= N; it may be
+ * problem i's own output (in place, ldr == ldo) but must not overlap any
+ * other output. gates[i].gate is one row of N values of out_dtype (the same
+ * gate for every row). Same requirements as dc_w8a8_gemm_grouped otherwise.
+ */
+typedef struct dc_gemm_gate {
+  const void* res;     /* [M, N] of out_dtype, row stride ldr */
+  int64_t ldr;
+  const void* gate;    /* [N] of out_dtype */
+} dc_gemm_gate;
+int dc_w8a8_gemm_grouped_gated(const dc_gemm_problem* problems, const dc_gemm_gate* gates, int count, int64_t N,
+                               int64_t K, int bias_dtype, int out_dtype, void* stream);
+
+/*
  * Whether one dc_w8a8_gemm_grouped launch over problems of these row counts
  * is expected to beat separate dc_w8a8_gemm calls on the current device: 1
  * when K % 256 == 0, there are at least two non-empty problems and their

@@ -54,11 +54,15 @@ class Prob(ctypes.Structure):
     _fields_ = [("a", P), ("lda", I64), ("w", P), ("ldw", I64), ("sx", P), ("sw", P), ("bias", P), ("out", P),
                 ("ldo", I64), ("M", I64)]
 grp = sig("dc_w8a8_gemm_grouped", I, [P, I, I64, I64, I, I, P])
+class Gate(ctypes.Structure):
+    _fields_ = [("res", P), ("ldr", I64), ("gate", P)]
+ggrp = sig("dc_w8a8_gemm_grouped_gated", I, [P, P, I, I64, I64, I, I, P])
 gplan = sig("dc_w8a8_gemm_group_plan", I, [ctypes.POINTER(I64), I, I64, I64])
 BF16, F16, F32 = 1, 0, 2
 probs = (Prob * 4)(Prob(16, 512, 16, 512, 16, 16, None, 16, 3072, 64), Prob(16, 500, 16, 512, 16, 16, None, 16, 3072, 64),
                    Prob(16, 512, None, 512, 16, 16, None, 16, 3072, 64), Prob(16, 512, 16, 512, 16, 16, None, 16, 3072, 0))
 Ms = (I64 * 4)(4096, 512, 0, 77)
+gates = (Gate * 4)(Gate(16, 3072, 16), Gate(None, 3072, 16), Gate(16, 3000, 16), Gate(None, 0, None))
 st = (I64 * 3)(8, 8, 8)
 bad = (I64 * 3)(8, 12, 8)
 checks = [
@@ -93,6 +97,12 @@ checks = [
     (grp(probs, 2, 3072, 512, -1, BF16, None), 2),
     (grp(ctypes.byref(probs, 2 * ctypes.sizeof(Prob)), 2, 3072, 512, -1, BF16, None), 1),
     (grp(ctypes.byref(probs, 3 * ctypes.sizeof(Prob)), 1, 3072, 512, -1, BF16, None), 0),
+    (ggrp(probs, None, 1, 3072, 512, -1, BF16, None), 1),
+    (ggrp(probs, gates, 1, 3072, 512, -1, 3, None), 1),
+    (ggrp(ctypes.byref(probs, 0), ctypes.byref(gates, ctypes.sizeof(Gate)), 1, 3072, 512, -1, BF16, None), 1),
+    (ggrp(ctypes.byref(probs, 0), ctypes.byref(gates, 2 * ctypes.sizeof(Gate)), 1, 3072, 512, -1, BF16, None), 1),
+    (ggrp(ctypes.byref(probs, 3 * ctypes.sizeof(Prob)), ctypes.byref(gates, 3 * ctypes.sizeof(Gate)), 1, 3072, 512,
+          -1, BF16, None), 0),
     (gplan(Ms, 4, 3072, 3072), 1),
     (gplan(Ms, 9, 3072, 3072), -1),
 ]

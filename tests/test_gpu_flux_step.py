@@ -10,8 +10,8 @@ Two comparisons, on the same seeded weights and inputs:
        and on the 4-step final latent;
   (ii) the INT8 step with the fused glue passes against the INT8 step with
        the reference's eager glue (LayerNorm-modulate, QK RMSNorm + rotary,
-       GELU, concatenation as torch ops): the same int8 weights, so only the
-       glue's rounding differs.
+       GELU, concatenation, gate and residual as torch ops; ``fused_glue``
+       off): the same int8 weights, so only the glue's rounding differs.
 The bounds are stated in each test; the measured values are printed.
 """
 

@@ -4,12 +4,14 @@ exact and the fused epilogue rounds bit for bit like ``rescale(int_mm())``
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 import torch.nn as nn
 
-from diffucore_amd import _int8
+from diffucore_amd import _int8, _lib
 from oracle import gemm as OG
 from oracle import quant as OQ
 from tests._util import DT, np32, rel_l2
@@ -282,3 +284,91 @@ def test_group_plan_and_layers(gpu):
     xb = torch.randn(1, 512, 3072, device=gpu).to(torch.bfloat16)
     ya, yb = _int8.linear_group([la, lb], [xa, xb])
     assert torch.equal(ya, la(xa)) and torch.equal(yb, lb(xb))
+
+
+GATED = [([4096, 512], 3072, 3072), ([300], 1000, 768), ([257, 0, 513, 64], 640, 256), ([4608], 3072, 1024)]
+
+
+def _res_gate(m, n, dtype, gpu, seed):
+    g = torch.Generator().manual_seed(seed)
+    return ((torch.randn(m, n, generator=g) * 2).to(dtype).to(gpu), (torch.randn(n, generator=g)).to(dtype).to(gpu))
+
+
+@pytest.mark.parametrize("ms,n,k", GATED)
+@pytest.mark.parametrize("dtype,bias_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, None),
+                                              (torch.float32, torch.float32), (torch.bfloat16, torch.float32)])
+def test_gated_grouped_gemm_equals_torch_ops(gpu, ms, n, k, dtype, bias_dtype):
+    """dc_w8a8_gemm_grouped_gated: each output bit-identical to torch's
+    res + gate * y on the plain grouped GEMM's y (FLUX's x + gate * out,
+    reference flux_dit.py:298-301, 336), full and partial tiles."""
+    items, gates = [], []
+    for i, m in enumerate(ms):
+        q, w, sx, sw = _qw(m, n, k, 60 + i)
+        b = (torch.randn(n, generator=torch.Generator().manual_seed(70 + i)) * 0.5).to(bias_dtype) \
+            if bias_dtype is not None else None
+        items.append((q.to(gpu), w.to(gpu), sx.to(gpu), sw.to(gpu), b.to(gpu) if b is not None else None))
+        gates.append(_res_gate(m, n, dtype, gpu, 80 + i))
+    ys = _int8._gemm_grouped(items, dtype)
+    outs = _int8._gemm_grouped(items, dtype, gates)
+    for m, y, out, (res, gate) in zip(ms, ys, outs, gates):
+        assert out.shape == (m, n) and out.dtype == dtype
+        assert torch.equal(out, res + gate * y)
+
+
+def test_gated_gemm_in_place_and_strided_residual(gpu):
+    """The residual may be the output itself (in place), or a strided view."""
+    n, k, dtype = 1024, 512, torch.bfloat16
+    q, w, sx, sw = (t.to(gpu) for t in _qw(1000, n, k, 90))
+    bias = torch.randn(n, device=gpu).to(dtype)
+    y = _int8._gemm_grouped([(q, w, sx, sw, bias)], dtype)[0]
+    res, gate = _res_gate(1000, n, dtype, gpu, 91)
+    want = res + gate * y
+    so = _lib.require()
+    prob = _lib.GemmProblem(q.data_ptr(), q.stride(0), w.data_ptr(), w.stride(0), sx.data_ptr(), sw.data_ptr(),
+                            bias.data_ptr(), res.data_ptr(), n, 1000)
+    gt = _lib.GemmGate(res.data_ptr(), n, gate.data_ptr())
+    rc = so.dc_w8a8_gemm_grouped_gated(ctypes.byref(prob), ctypes.byref(gt), 1, n, k, _lib.BF16, _lib.BF16,
+                                       _lib.stream_ptr(gpu))
+    assert rc == 0, so.dc_last_error()
+    assert torch.equal(res, want)
+    wide = torch.randn(1000, 2 * n, device=gpu).to(dtype)
+    out = _int8._gemm_grouped([(q, w, sx, sw, bias)], dtype, [(wide[:, 64:64 + n], gate)])[0]
+    assert torch.equal(out, wide[:, 64:64 + n] + gate * y)
+
+
+def test_matmul_quantized_gated_layers(gpu):
+    """The layer-level helper: fused (grouped pair; one layer whose plan is
+    the DMA-fed kernel) and fallback (a plan that is not) all equal the
+    reference's x + gate * layer(x') torch ops, with FLUX's [B, L, N]
+    residual and [B, 1, N] gate."""
+    torch.manual_seed(5)
+    bf = torch.bfloat16
+    la = _int8.Int8Linear.from_linear(nn.Linear(3072, 3072).to(gpu).to(bf), 256)
+    lb = _int8.Int8Linear.from_linear(nn.Linear(3072, 3072).to(gpu).to(bf), 256)
+    xa, xb = torch.randn(1, 4096, 3072, device=gpu).to(bf), torch.randn(1, 512, 3072, device=gpu).to(bf)
+    ra, rb = torch.randn(1, 4096, 3072, device=gpu).to(bf), torch.randn(1, 512, 3072, device=gpu).to(bf)
+    ga, gb = torch.randn(1, 1, 3072, device=gpu).to(bf), torch.randn(1, 1, 3072, device=gpu).to(bf)
+    qa = _int8.quantize_activation(xa.reshape(-1, 3072), 256)
+    qb = _int8.quantize_activation(xb.reshape(-1, 3072), 256)
+    assert _int8.gemm_group_plan([4096, 512], 3072, 3072) or \
+        torch.cuda.get_device_properties(gpu).multi_processor_count != 256
+    ya, yb = _int8.matmul_quantized_gated([(la, *qa, ra, ga), (lb, *qb, rb, gb)], bf)
+    assert torch.equal(ya.view(ra.shape), ra + ga * la(xa)) and torch.equal(yb.view(rb.shape), rb + gb * lb(xb))
+    # one layer: FLUX's linear2 shape, whose plan is the DMA-fed kernel (fused),
+    # and the 512-row text layer, whose plan is not (GEMM, then torch ops)
+    lc = _int8.Int8Linear.from_linear(nn.Linear(15360, 3072).to(gpu).to(bf), 256)
+    xc = torch.randn(1, 4608, 15360, device=gpu).to(bf)
+    rc, gc = torch.randn(1, 4608, 3072, device=gpu).to(bf), torch.randn(1, 1, 3072, device=gpu).to(bf)
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert _int8.gemm_plan(4608, 3072, 15360) == "dma_256x256" and _int8.gemm_plan(512, 3072, 3072) != "dma_256x256"
+    qc = _int8.quantize_activation(xc.reshape(-1, 15360), 256)
+    (y1,) = _int8.matmul_quantized_gated([(lc, *qc, rc, gc)], bf)
+    assert torch.equal(y1.view(rc.shape), rc + gc * lc(xc))
+    (y2,) = _int8.matmul_quantized_gated([(lb, *qb, rb, gb)], bf)
+    assert torch.equal(y2.view(rb.shape), rb + gb * lb(xb))
+    # a gate per sample (B = 2) is not one row: the torch ops, same values
+    x2, r2 = torch.randn(2, 256, 3072, device=gpu).to(bf), torch.randn(2, 256, 3072, device=gpu).to(bf)
+    g2 = torch.randn(2, 1, 3072, device=gpu).to(bf)
+    q2 = _int8.quantize_activation(x2.reshape(-1, 3072), 256)
+    (y3,) = _int8.matmul_quantized_gated([(la, *q2, r2, g2)], bf)
+    assert torch.equal(y3.view(r2.shape), r2 + g2 * la(x2))

@@ -7,7 +7,8 @@ captured input buffers must reach the next replay.
 
 Covered: the quantize kernel, each GEMM plan the FLUX step uses (DMA-fed
 256 x 256, 192 x 256 / 128 x 128, split-K with its workspace and epilogue
-pass, a grouped launch of two layers) and the INT8 attention (K statistics, K quantize, attention): the
+pass, a grouped launch of two layers, the same pair with the gated
+residual epilogue) and the INT8 attention (K statistics, K quantize, attention): the
 256-query kernel at the FLUX shape, stream-K pieces and their merge at SDXL's
 4096-token self-attention, and the 128-query kernel whole.
 """
@@ -34,6 +35,9 @@ def _case(gpu, seed):
     torch.manual_seed(seed)
     layers = [_int8.Int8Linear.from_linear(nn.Linear(k, n, bias=True).to(gpu).to(BF16), 256) for _, k, n in LINEARS]
     xs = [torch.randn(m, k, generator=g, device=gpu).to(BF16) for m, k, _ in LINEARS]
+    # residuals and one-row gates for the gated pair (the last two layers)
+    xs += [torch.randn(m, n, generator=g, device=gpu).to(BF16) for m, _, n in LINEARS[3:]]
+    xs += [torch.randn(n, generator=g, device=gpu).to(BF16) for _, _, n in LINEARS[3:]]
     qkvs = [[torch.randn(b, h, l, d, generator=g, device=gpu).to(BF16) for _ in range(3)] for b, h, l, d in ATTN]
     return layers, xs, qkvs
 
@@ -41,7 +45,10 @@ def _case(gpu, seed):
 def _step(layers, xs, qkvs):
     ys = [layer.matmul_quantized(*_int8.quantize_activation(x, layer.group), BF16)
           for layer, x in zip(layers[:3], xs[:3])]
-    ys += _int8.linear_group(layers[3:], xs[3:])
+    ys += _int8.linear_group(layers[3:], xs[3:5])
+    qs = [_int8.quantize_activation(x, layer.group) for layer, x in zip(layers[3:], xs[3:5])]
+    ys += _int8.matmul_quantized_gated([(layer, *q, r, gt) for layer, q, r, gt in zip(layers[3:], qs, xs[5:7], xs[7:9])],
+                                       BF16)
     return ys + [attention_bhld(q, k, v, "int8_turing") for q, k, v in qkvs]
 
 
@@ -50,6 +57,7 @@ def test_graph_replays_equal_eager_calls(gpu):
     m, k, n = LINEARS[0]
     assert _int8.gemm_plan(m, n, k) == "dma_256x256"
     assert _int8.gemm_group_plan([LINEARS[3][0], LINEARS[4][0]], LINEARS[3][2], LINEARS[3][1])
+    assert all(x.data_ptr() % 16 == 0 for x in xs[5:])   # the gated pair takes the fused epilogue
     with torch.no_grad():
         want = [t.clone() for t in _step(layers, xs, qkvs)]
         side = torch.cuda.Stream()

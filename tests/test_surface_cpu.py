@@ -299,6 +299,19 @@ def test_argument_checks_fail_before_any_launch():
     assert so.dc_w8a8_gemm_grouped(bad, 1, 3072, 512, -1, _lib.BF16, None) == 1 and b"ldo" in so.dc_last_error()
     empty = (P * 2)(P(16, 512, 16, 512, 16, 16, None, 16, 3072, 0), P(None, 0, None, 0, None, None, None, None, 0, 0))
     assert so.dc_w8a8_gemm_grouped(empty, 2, 3072, 512, -1, _lib.BF16, None) == 0       # nothing to run
+    # dc_w8a8_gemm_grouped_gated: the gates array, a float output, each residual and gate
+    G = _lib.GemmGate
+    gates = (G * 2)(G(16, 3072, 16), G(16, 3072, 16))
+    gated = so.dc_w8a8_gemm_grouped_gated
+    assert gated(probs, None, 2, 3072, 512, -1, _lib.BF16, None) == 1 and b"null" in so.dc_last_error()
+    assert gated(probs, gates, 2, 3072, 512, -1, _lib.I32, None) == 1 and b"out_dtype" in so.dc_last_error()
+    assert gated(probs, gates, 2, 3072, 320, -1, _lib.BF16, None) == 2 and b"256" in so.dc_last_error()
+    assert gated(probs, (G * 2)(G(16, 3072, 16), G(None, 3072, 16)), 2, 3072, 512, -1, _lib.BF16, None) == 1
+    assert b"residual or gate" in so.dc_last_error()
+    assert gated(probs, (G * 2)(G(16, 3072, 16), G(16, 3072, None)), 2, 3072, 512, -1, _lib.BF16, None) == 1
+    assert gated(probs, (G * 2)(G(16, 3000, 16), G(16, 3072, 16)), 2, 3072, 512, -1, _lib.BF16, None) == 1
+    assert b"ldr" in so.dc_last_error()
+    assert gated(empty, (G * 2)(G(None, 0, None), G(None, 0, None)), 2, 3072, 512, -1, _lib.BF16, None) == 0
     # the group plan (256 CUs when no device answers): FLUX's double-block pairs
     Ms = (_lib.ctypes.c_int64 * 2)(4096, 512)
     assert so.dc_w8a8_gemm_group_plan(Ms, 2, 9216, 3072) == 1          # 576 + 72 tiles: 3 rounds either way
