@@ -807,6 +807,20 @@ constexpr int WIDE_MAX_TILES = 2048;                // K block scales staged in 
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr_t;
 
+// One DMA of 16 bytes per lane from global memory into LDS
+// (global_load_lds_dwordx4 from the wave-uniform address `base` plus the
+// lane's byte offset `off`; lane i's bytes land at m0 + 16 i, `lds` being the
+// wave's LDS destination). Inline asm, so the compiler's wait-count pass does
+// not see an LDS store: it cannot tell the ring stages apart and otherwise
+// waits for every DMA in flight (vmcnt(0)) before some of the next tile's LDS
+// reads, which measured 3% of the kernel's time at the FLUX shape. The kernel
+// orders each stage's writes and reads itself, by vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, const void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)reinterpret_cast<uintptr_t>((lds_void_ptr_t)(const_cast<void*>(lds))));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(m0) : "memory");
+}
+
 // The 8 K operands (k-step ks, key block kb) of one 64-key tile from a
 // swizzled K stage; kfo[ks] is the lane's byte offset of its 16-byte chunk for
 // k-step ks (row l32).
@@ -874,25 +888,22 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
   }
   // tile `tile` into stage `st` (tile % STAGES); past the end the source is
   // the last tile again (in bounds; that data is never read)
-  const uint8_t* kgw = reinterpret_cast<const uint8_t*>(kg) + koff;
   auto issue = [&](int tile, int st) __attribute__((always_inline)) {
     uint8_t* sb = lds + st * WSTAGE;
     tile = min(tile, ntiles - 1);
-    __builtin_amdgcn_global_load_lds(kgw + tile * (BKEY * 128), (lds_void_ptr_t)(sb + 1024 * w), 16, 0, 0);
+    dma16(reinterpret_cast<const uint8_t*>(kg) + tile * (BKEY * 128), koff, sb + 1024 * w);
     uint8_t* sv = sb + WK_BYTES;
+    const uint16_t* vt = vg + (int64_t)tile * BKEY * p.vsl;
     if (ragged && tile == ntiles - 1) {
       // keys past Lk read key Lk - 1 (their probabilities are 0; the values stay finite)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int key = min(tile * BKEY + vrow[u], p.Lk - 1);
-        __builtin_amdgcn_global_load_lds(vg + (int64_t)key * p.vsl + vcol[u],
-                                         (lds_void_ptr_t)(sv + 1024 * (w + 8 * u)), 16, 0, 0);
+        const int key = min(tile * BKEY + vrow[u], p.Lk - 1) - tile * BKEY;
+        dma16(vt, (uint32_t)(key * (int)p.vsl + vcol[u]) * 2u, sv + 1024 * (w + 8 * u));
       }
     } else {
-      const uint8_t* vt = reinterpret_cast<const uint8_t*>(vg + (int64_t)tile * BKEY * p.vsl);
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-        __builtin_amdgcn_global_load_lds(vt + voff[u], (lds_void_ptr_t)(sv + 1024 * (w + 8 * u)), 16, 0, 0);
+      for (int u = 0; u < 2; ++u) dma16(vt, voff[u], sv + 1024 * (w + 8 * u));
     }
   };
 
