@@ -314,58 +314,11 @@ __device__ __forceinline__ void qk_tile(const uint8_t* __restrict__ sK, int klan
 
 __device__ __forceinline__ int max3i(int a, int b, int c) { return max(max(a, b), c); }
 
-// Online softmax of one tile, in three parts so the QK^T MFMAs of the next
-// tile can be issued between the first and the second. key0 is the key of
-// register 0 of block 0 for this lane (tile start + 4 hf); TAIL masks keys >= Lk.
-//
-// Part 1: tile row maximum, rescale of O and the row sum when it grows by more
-// than 2^8 (P = 2^(logit - m) may reach 2^8 before the running max is moved:
-// O / sum(P) does not depend on m and float32 has the range). Returns the
-// exponent scale c; `bias` is set so that P = 2^(bits(S) * c - bias).
-template <int DP, bool TAIL>
-__device__ __forceinline__ float softmax_max(v16i (&s)[2], int key0, int Lk, float ksc, float cq, float& m, float& lsum,
-                                             v16f (&o)[DP / 32], float& bias) {
-  constexpr int ND = DP / 32;
-  if constexpr (TAIL) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (key0 + 32 * kb + 8 * (j >> 2) + (j & 3) >= Lk) s[kb][j] = INT_MIN;
-  }
-  // the scores carry the bits of 12582912 + S: integer order is float order;
-  // four independent max3 chains, then the lane halves (same query row, the
-  // other keys) exchanged with v_permlane32_swap instead of an LDS permute
-  int mq[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int kb = c >> 1, j0 = 8 * (c & 1);
-    mq[c] = max3i(s[kb][j0], s[kb][j0 + 1], s[kb][j0 + 2]);
-    mq[c] = max3i(mq[c], s[kb][j0 + 3], s[kb][j0 + 4]);
-    mq[c] = max3i(mq[c], s[kb][j0 + 5], s[kb][j0 + 6]);
-    mq[c] = max(mq[c], s[kb][j0 + 7]);
-  }
-  int mx = max(max(mq[0], mq[1]), max(mq[2], mq[3]));
-  const auto halves = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
-  mx = max((int)halves[0], (int)halves[1]);
-
-  const float c = cq * ksc;
-  const float mt = (__int_as_float(mx) - MAGIC_F) * c;
-  if (__any(mt > m + 8.0f)) {
-    const float mnew = fmaxf(m, mt);
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-    lsum *= alpha;
-#pragma unroll
-    for (int i = 0; i < ND; ++i)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) o[i][j] *= alpha;
-    m = mnew;
-  }
-  bias = __builtin_fmaf(MAGIC_F, c, m);
-  return c;
-}
-
-// Part 2: P as 16-bit pairs, and its row sum.
+// Online softmax of one tile: P = 2^(bits(S) * c - bias) as 16-bit pairs (bias
+// = MAGIC_F c + m: the scores carry the bits of 12582912 + S), and its sum
+// added to lsum (the packed values, v_dot2c against (1, 1)). key0 is the key
+// of register 0 of block 0 for this lane (tile start + 4 hf); TAIL zeroes keys
+// >= Lk.
 template <int DT, bool TAIL>
 __device__ __forceinline__ void softmax_exp(const v16i (&s)[2], int key0, int Lk, float c, float bias, float& lsum,
                                             uint32_t (&pk)[2][8]) {
@@ -384,7 +337,7 @@ __device__ __forceinline__ void softmax_exp(const v16i (&s)[2], int key0, int Lk
     }
 }
 
-// Part 3: O^T[d][q] += V^T[d][keys] P^T[keys][q], 16 keys per MFMA.
+// O^T[d][q] += V^T[d][keys] P^T[keys][q], 16 keys per MFMA.
 template <int DT, int DP>
 __device__ __forceinline__ void pv_tile(const uint32_t (&pk)[2][8], const uint8_t* __restrict__ sV, int vlane,
                                         v16f (&o)[DP / 32]) {
@@ -408,14 +361,72 @@ __device__ __forceinline__ void pv_tile(const uint32_t (&pk)[2][8], const uint8_
   }
 }
 
+// Largest probability a tile may hold before the running maximum moves:
+// P = 2^(logit - m) <= 2^12 keeps float16 P (max 65504) and float32 O and row
+// sums in range. O / sum(P) does not depend on m.
+constexpr float P_LIMIT = 4096.f;
+
+// Exact maximum logit of the lane's query row over the tile. The scores carry
+// the bits of 12582912 + S, positive floats, so integer order is float order:
+// four independent max3 chains, then the lane halves (same query row, the
+// other keys) exchanged with v_permlane32_swap. TAIL excludes keys >= Lk
+// (their scores are overwritten).
+template <bool TAIL>
+__device__ __forceinline__ float tile_max(v16i (&s)[2], int key0, int Lk, float c) {
+  if constexpr (TAIL) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (key0 + 32 * kb + 8 * (j >> 2) + (j & 3) >= Lk) s[kb][j] = INT_MIN;
+  }
+  int mq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int kb = q >> 1, j0 = 8 * (q & 1);
+    mq[q] = max3i(s[kb][j0], s[kb][j0 + 1], s[kb][j0 + 2]);
+    mq[q] = max3i(mq[q], s[kb][j0 + 3], s[kb][j0 + 4]);
+    mq[q] = max3i(mq[q], s[kb][j0 + 5], s[kb][j0 + 6]);
+    mq[q] = max(mq[q], s[kb][j0 + 7]);
+  }
+  int mx = max(max(mq[0], mq[1]), max(mq[2], mq[3]));
+  const auto halves = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+  mx = max((int)halves[0], (int)halves[1]);
+  return (__int_as_float(mx) - MAGIC_F) * c;
+}
+
+// Lazy row maximum. The tile's P was taken against the running maximum m
+// (bias = MAGIC_F c + m) and `ts` holds the lane's sum of it. When some lane's
+// sum exceeds P_LIMIT (so a probability may exceed it), or at the first tile
+// (m = -inf gives infinities), m moves to the exact maximum, the row sum and
+// O are rescaled and P is recomputed. Then ts joins the row sum.
+template <int DT, int DP, bool TAIL>
+__device__ __forceinline__ void lazy_fixup(v16i (&s)[2], int key0, int Lk, float c, float& m, float& lsum, float ts,
+                                           v16f (&o)[DP / 32], uint32_t (&pk)[2][8]) {
+  if (__any(!(ts <= P_LIMIT))) {
+    const float mnew = fmaxf(m, tile_max<TAIL>(s, key0, Lk, c));
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    lsum *= alpha;
+#pragma unroll
+    for (int i = 0; i < DP / 32; ++i)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[i][j] *= alpha;
+    ts = 0.f;
+    softmax_exp<DT, TAIL>(s, key0, Lk, c, __builtin_fmaf(MAGIC_F, c, m), ts, pk);
+  }
+  lsum += ts;
+}
+
 // One tile's softmax and PV without a following tile to overlap.
 template <int DT, int DP, bool TAIL>
 __device__ __forceinline__ void softmax_pv(v16i (&s)[2], const uint8_t* __restrict__ sV, int vlane, int key0, int Lk,
                                            float ksc, float cq, float& m, float& lsum, v16f (&o)[DP / 32]) {
-  float bias;
-  const float c = softmax_max<DP, TAIL>(s, key0, Lk, ksc, cq, m, lsum, o, bias);
+  const float c = cq * ksc;
   uint32_t pk[2][8];
-  softmax_exp<DT, TAIL>(s, key0, Lk, c, bias, lsum, pk);
+  float ts = 0.f;
+  softmax_exp<DT, TAIL>(s, key0, Lk, c, __builtin_fmaf(MAGIC_F, c, m), ts, pk);
+  lazy_fixup<DT, DP, TAIL>(s, key0, Lk, c, m, lsum, ts, o, pk);
   pv_tile<DT, DP>(pk, sV, vlane, o);
 }
 
@@ -562,17 +573,18 @@ __device__ __forceinline__ void attn_piece(const AttnArgs& p, uint8_t* smem, int
     const int tl_ = (tile_);                                                                             \
     const int st_ = (tl_ - tb) & 1;                                                                      \
     const int key0_ = tl_ * BKEY + 4 * hf;                                                               \
-    float bias_;                                                                                         \
-    const float c_ = softmax_max<DP, false>(cur_, key0_, p.Lk, ksp[tl_], cq, m, lsum, o, bias_);         \
-    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    const float c_ = cq * ksp[tl_];                                                                      \
     uint32_t pk_[2][8];                                                                                  \
+    float ts_ = 0.f;                                                                                     \
     qk_tile<DP>(SK_STAGE(st_ ^ 1), klane, qf, next_);                                                    \
-    softmax_exp<DT, false>(cur_, key0_, p.Lk, c_, bias_, lsum, pk_);                                     \
+    softmax_exp<DT, false>(cur_, key0_, p.Lk, c_, __builtin_fmaf(MAGIC_F, c_, m), ts_, pk_);             \
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * ND, 0);                                              \
     _Pragma("unroll") for (int z_ = 0; z_ < 2 * ND; ++z_) {                                              \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                 \
       __builtin_amdgcn_sched_group_barrier(0x402, 96 / (2 * ND), 0);                                     \
     }                                                                                                    \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+    lazy_fixup<DT, DP, false>(cur_, key0_, p.Lk, c_, m, lsum, ts_, o, pk_);                              \
     __builtin_amdgcn_sched_barrier(0);                                                                   \
     pv_tile<DT, DP>(pk_, SV_STAGE(st_), vlane, o);                                                       \
     __builtin_amdgcn_sched_barrier(0);                                                                   \
@@ -810,15 +822,21 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr_t;
 // One DMA of 16 bytes per lane from global memory into LDS
 // (global_load_lds_dwordx4 from the wave-uniform address `base` plus the
 // lane's byte offset `off`; lane i's bytes land at m0 + 16 i, `lds` being the
-// wave's LDS destination). Inline asm, so the compiler's wait-count pass does
-// not see an LDS store: it cannot tell the ring stages apart and otherwise
-// waits for every DMA in flight (vmcnt(0)) before some of the next tile's LDS
-// reads, which measured 3% of the kernel's time at the FLUX shape. The kernel
-// orders each stage's writes and reads itself, by vmcnt waits and barriers.
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, const void* lds) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      (uint32_t)reinterpret_cast<uintptr_t>((lds_void_ptr_t)(const_cast<void*>(lds))));
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(m0) : "memory");
+// wave's LDS destination, a byte address in the LDS address space). Inline
+// asm, so the compiler's wait-count pass does not see an LDS store: it cannot
+// tell the ring stages apart and otherwise waits for every DMA in flight
+// (vmcnt(0)) before some of the next tile's LDS reads, which measured 3% of
+// the kernel's time at the FLUX shape. The kernel orders each stage's writes
+// and reads itself, by vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_ptr_t)(const_cast<void*>(p)));
 }
 
 // The 8 K operands (k-step ks, key block kb) of one 64-key tile from a
@@ -857,6 +875,7 @@ __device__ __forceinline__ v4i v_operand(const uint8_t* __restrict__ sV, const i
 // V operands are read VPRE MFMAs ahead of their use
 constexpr int VPRE = 4;
 
+
 template <int DT>
 __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[ATTN_WIDE_LDS];
@@ -888,22 +907,23 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
   }
   // tile `tile` into stage `st` (tile % STAGES); past the end the source is
   // the last tile again (in bounds; that data is never read)
+  // the wave's DMA destinations in stage 0 (K, then V rows of u = 0, 1)
+  const uint32_t lds0 = lds_addr(lds) + 1024 * w;
   auto issue = [&](int tile, int st) __attribute__((always_inline)) {
-    uint8_t* sb = lds + st * WSTAGE;
+    const uint32_t sb = lds0 + st * WSTAGE;
     tile = min(tile, ntiles - 1);
-    dma16(reinterpret_cast<const uint8_t*>(kg) + tile * (BKEY * 128), koff, sb + 1024 * w);
-    uint8_t* sv = sb + WK_BYTES;
+    dma16(reinterpret_cast<const uint8_t*>(kg) + tile * (BKEY * 128), koff, sb);
     const uint16_t* vt = vg + (int64_t)tile * BKEY * p.vsl;
     if (ragged && tile == ntiles - 1) {
       // keys past Lk read key Lk - 1 (their probabilities are 0; the values stay finite)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int key = min(tile * BKEY + vrow[u], p.Lk - 1) - tile * BKEY;
-        dma16(vt, (uint32_t)(key * (int)p.vsl + vcol[u]) * 2u, sv + 1024 * (w + 8 * u));
+        dma16(vt, (uint32_t)(key * (int)p.vsl + vcol[u]) * 2u, sb + WK_BYTES + 8192 * u);
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) dma16(vt, voff[u], sv + 1024 * (w + 8 * u));
+      for (int u = 0; u < 2; ++u) dma16(vt, voff[u], sb + WK_BYTES + 8192 * u);
     }
   };
 
@@ -971,12 +991,11 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
     for (int f = 0; f < VPRE; ++f) va[f] = v_operand(sv, vfo, f);
     __builtin_amdgcn_sched_barrier(0);
     const int key0 = tile * BKEY + 4 * hf;
-    float bias;
-    const float c = softmax_max<128, TAIL>(cur, key0, p.Lk, ks_l[tile], cq, m, lsum, o, bias);
-    __builtin_amdgcn_sched_barrier(0);
+    const float c = cq * ks_l[tile];
     uint32_t pk[2][8];
+    float ts = 0.f;
     qk_mfma(ka, qf, magic, nxt);
-    softmax_exp<DT, TAIL>(cur, key0, p.Lk, c, bias, lsum, pk);
+    softmax_exp<DT, TAIL>(cur, key0, p.Lk, c, __builtin_fmaf(MAGIC_F, c, m), ts, pk);
     // the 8 QK^T MFMAs with 12 of the ~100 VALU instructions of the
     // exponentials behind each
 #pragma unroll
@@ -984,6 +1003,8 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    lazy_fixup<DT, 128, TAIL>(cur, key0, p.Lk, c, m, lsum, ts, o, pk);
     __builtin_amdgcn_sched_barrier(0);
     // PV: MFMA f consumes V operand f, read VPRE MFMAs earlier
 #pragma unroll

@@ -80,6 +80,32 @@ def test_wide_cases_run_256_query_tiles(gpu, B, Lq, Lk, H, D, dtype):
     assert A.attn_plan(1, 4, 1024, 1024, 128, dtype) == {"dp_tiles": 32, "sk_blocks": 0, "sk_tiles": 0}
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wide_kernel_growing_logits_rescale(gpu, dtype):
+    """Keys aligned ever more with the queries: the row maxima grow by ~6 (log2
+    units) per 64-key tile, from ~8 in the first tile to ~100 in the last, so
+    the wide kernel's lazy maximum (P against the running maximum, rescaled
+    when a tile's probabilities sum past 2^12) rescales O every few tiles; in
+    float16 an unrescaled P would overflow. Against the oracle's exact online
+    softmax."""
+    B, Lq, Lk, H, D = 1, 1024, 1024, 64, 128
+    g = torch.Generator().manual_seed(3)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = (8 * u + 0.1 * torch.randn(B, Lq, H, D, generator=g)).to(dtype)
+    k = (100 * torch.linspace(0, 1, Lk).view(1, Lk, 1, 1) * u + torch.randn(B, Lk, H, D, generator=g)).to(dtype)
+    v = torch.randn(B, Lk, H, D, generator=g).to(dtype)
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert A.attn_plan(B, H, Lq, Lk, D, dtype)["dp_tiles"] == 256   # whole 256-query tiles
+    out, _ = _run(q, k, v, gpu)
+    o = np32(out)
+    assert np.isfinite(o).all()
+    ora = OA.int8_attention(np32(q), np32(k), np32(v), D ** -0.5, DT[dtype], DT[dtype])
+    r, c = rel_l2(o, ora), cosine(o, ora)
+    print(f"[attn] growing logits {DT[dtype]}: vs oracle rel {r:.2e} cos {c:.7f}")
+    assert r < ORACLE_REL[dtype] and c > ORACLE_COS
+
+
 @pytest.mark.parametrize("B,Lq,Lk,H,D,dtype", CASES)
 def test_codes_and_scales_bit_exact(gpu, B, Lq, Lk, H, D, dtype):
     q, k, v = _inputs(B, Lq, Lk, H, D, dtype)
