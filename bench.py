@@ -26,16 +26,20 @@ The same run also measures, and adds to the JSON line:
     attention + W8A8 linears against the same step with bf16 SDPA and bf16
     linears, ms per step and the final-latent deviation after 4 steps;
   * the reference's CPU path (torch CPU ops, oracle/cpu_path.py) on a bounded
-    row sample of the same workload.
+    row sample of the same workload;
+  * the MFMA-only throughput this device sustains (dc_mfma_probe), next to
+    the published peak in the roofline object.
 
     python bench.py [--steps K] [--warmup W] [--no-full] [--no-cpu]
     python bench.py --copy-calibration   # 1 GiB device copy for counter scaling
+    python bench.py --mfma-ceiling       # MFMA-only throughput (int8, bf16)
     python bench.py --shapes             # per-shape report for every BASELINE config
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import hashlib
 import json
 import os
@@ -206,6 +210,41 @@ def copy_calibration(mib: int = 1024, reps: int = 5):
 
 
 # ---------------------------------------------------------------- CPU baseline
+
+def mfma_ceiling(iters: int = 100000) -> dict:
+    """Measured MFMA throughput of this device (dc_mfma_probe): back-to-back
+    independent MFMAs with nothing else in the loop, one workgroup per CU,
+    1 or 2 waves per SIMD, constant or changing operands. The published
+    peaks (int8 5.0 POP/s, bf16 2.5 PFLOP/s) assume the peak engine clock;
+    under this load the chip runs at its power limit, lower with operands that
+    change from one MFMA to the next (as real data does)."""
+    from diffucore_amd import _lib
+    L = _lib.require()
+    units = L.dc_mfma_probe_units()
+    sink = torch.empty(units * 8, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    out = {"units": units, "iters": iters, "what": "TOP/s (int8) and TFLOP/s (bf16) of back-to-back independent "
+           "MFMAs, one workgroup per CU; 'vary' = operands change every MFMA (per-lane hashed int8 codes / bf16 "
+           "values of magnitude 0.5-2), 'const' = one operand pair reused"}
+    for kind, name, per in ((0, "int8_32x32x32", 65536), (1, "bf16_32x32x16", 32768)):
+        for vary in (0, 1):
+            for waves in (1, 2):
+                def launch(n):
+                    rc = L.dc_mfma_probe(kind, vary, waves, n, ctypes.c_void_p(sink.data_ptr()),
+                                         ctypes.c_void_p(stream.cuda_stream))
+                    if rc:
+                        raise RuntimeError(L.dc_last_error().decode())
+                launch(iters // 10)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                launch(iters)
+                e1.record()
+                torch.cuda.synchronize()
+                s = e0.elapsed_time(e1) * 1e-3
+                rate = units * 4 * waves * iters * 8 * per / s / 1e12
+                out[f"{name}_{'vary' if vary else 'const'}_{waves}w"] = round(rate, 1)
+    return out
+
 
 def cpu_baseline(shape, budget_s: float = 12.0, rows: int = 256):
     """The reference's CPU path (oracle/cpu_path.py) on a row sample of one
@@ -585,6 +624,9 @@ def main():
                     help="only run a 1 GiB device copy (scales the rocprofv3 byte counters) and exit")
     ap.add_argument("--shapes", action="store_true",
                     help="only print the per-shape report (every BASELINE config shape) and exit")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only measure the MFMA-only throughput of the device (int8 and bf16, 1 and 2 waves per "
+                         "SIMD, constant and changing operands) and exit")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only summarize rocprofv3 FETCH_SIZE / WRITE_SIZE runs under DIR (copy_* and step_*) "
                          "into profiles/gemm_flux_step_traffic.json and exit (no GPU)")
@@ -598,6 +640,10 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.mfma_ceiling:
+        torch.cuda.set_device(0)
+        print(json.dumps({"mfma_ceiling": mfma_ceiling()}), flush=True)
         return
     if args.shapes:
         from diffucore_amd import _lib
@@ -705,6 +751,11 @@ def main():
                 "algorithmic_bytes_per_launch": int(bytes_per_launch),
                 "avg_launch_us": round(1e6 * launch_s, 2),
                 "launches_timed": g["launches"]}
+    # the MFMA-only rate this device sustains (same process, after the steps)
+    ceiling = mfma_ceiling()
+    best = max(ceiling["int8_32x32x32_vary_1w"], ceiling["int8_32x32x32_vary_2w"])
+    roofline["measured_mfma_ceiling"] = best
+    roofline["frac_of_measured_ceiling"] = round(achieved / best, 4)
 
     result = {
         "metric": METRIC, "value": round(tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
@@ -718,6 +769,7 @@ def main():
         "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
         "kernels": kernels,
         "roofline": roofline,
+        "mfma_ceiling": ceiling,
     }
     result.update(extra)
     if not args.no_cpu:

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libdiffucore_amd.so"
 
 F16, BF16, F32, I32, NONE = 0, 1, 2, 3, -1
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _DTYPE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int32: I32}
 
@@ -50,6 +50,8 @@ _SIGS = {
                                       ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
                                       ctypes.POINTER(_I64), ctypes.c_float, _P]),
     "dc_int8_attn_quantize_q": (_I, [_P, _I, _I, _I, _I, _I, ctypes.POINTER(_I64), _P, _P, _P]),
+    "dc_mfma_probe": (_I, [_I, _I, _I, _I, _P, _P]),
+    "dc_mfma_probe_units": (_I, []),
 }
 SYMBOLS = tuple(_SIGS)
 

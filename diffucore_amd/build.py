@@ -11,12 +11,14 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libdiffucore_amd.so"
-SOURCES = ["quant.hip", "qknorm.hip", "gemm.hip", "attn.hip", "capi.cpp"]
+SOURCES = ["quant.hip", "qknorm.hip", "gemm.hip", "attn.hip", "calib.hip", "capi.cpp"]
 ARCH = "gfx950"
 
 FLAGS = [
@@ -39,15 +41,27 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (needs ROCm)")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into ``LIB`` (always recompiles)."""
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *FLAGS, "-o", str(tmp), *[str(CSRC / s) for s in SOURCES]]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into ``LIB`` (always recompiles): one object
+    per source, compiled in parallel, then linked."""
+    with tempfile.TemporaryDirectory(prefix="dc_build_") as tmpdir:
+        objs = [str(Path(tmpdir) / (Path(s).stem + ".o")) for s in SOURCES]
+        compile_flags = [f for f in FLAGS if f != "-shared"]
+        cmds = [[hipcc(), *compile_flags, "-c", "-o", o, str(CSRC / s)] for s, o in zip(SOURCES, objs)]
+        workers = max(1, min(len(cmds), os.cpu_count() or 1, 16))
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        tmp = LIB.with_suffix(".so.tmp")
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs], verbose)
     os.replace(tmp, LIB)
     return LIB
 

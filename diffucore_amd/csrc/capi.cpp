@@ -21,4 +21,4 @@ void clear_error() { g_err[0] = '\0'; }
 
 extern "C" const char* dc_last_error(void) { return dc::g_err; }
 
-extern "C" int dc_abi_version(void) { return 12; }
+extern "C" int dc_abi_version(void) { return 13; }

@@ -336,6 +336,21 @@ int dc_int8_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* 
 int dc_int8_attn_quantize_q(const void* q, int dtype, int B, int H, int Lq, int D,
                             const int64_t q_strides[3], int8_t* q8, float* qs, void* stream);
 
+/*
+ * MFMA throughput calibration (no counterpart in the reference; measurement
+ * only). Launches one workgroup per compute unit with `waves` (1 or 2) waves
+ * per SIMD, each issuing `iters` x 8 independent back-to-back MFMAs on 4
+ * accumulators: kind 0 v_mfma_i32_32x32x32_i8 (65536 ops each), kind 1
+ * v_mfma_f32_32x32x16_bf16 (32768 flops each); vary = 1 cycles each wave
+ * through 8 operand pairs of per-lane hashed values (uniform int8 codes, bf16
+ * magnitudes in [0.5, 2)), vary = 0 reuses one pair. Writes one int per wave
+ * to sink[units * 4 * waves] so the work is kept. The caller times the launch
+ * on `stream`; dc_mfma_probe_units() gives the unit count. Returns 0,
+ * DC_EINVAL or DC_EHIP.
+ */
+int dc_mfma_probe(int kind, int vary, int waves, int iters, int* sink, void* stream);
+int dc_mfma_probe_units(void);
+
 #ifdef __cplusplus
 }
 #endif

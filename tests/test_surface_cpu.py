@@ -251,6 +251,11 @@ def test_argument_checks_fail_before_any_launch():
     assert b"head dim" in so.dc_last_error()
     assert so.dc_int8_attn_fwd(16, 16, 16, 16, _lib.F32, 1, 1, 4, 4, 64, st, st, st, st, 0.1, 16, 1 << 20,
                                None) == 1
+    # the MFMA calibration probe: kind, vary, waves and iteration count checked before any HIP call
+    assert so.dc_mfma_probe(2, 0, 1, 10, 16, None) == 1 and b"kind" in so.dc_last_error()
+    assert so.dc_mfma_probe(0, 0, 3, 10, 16, None) == 1
+    assert so.dc_mfma_probe(1, 1, 1, 0, 16, None) == 1
+    assert so.dc_mfma_probe(0, 1, 2, 10, None, None) == 1 and b"null" in so.dc_last_error()
     # dc_qk_norm_rope: argument order (dtype, B, L, H, D, flags, eps, q, q_strides, q_weight, k, k_strides,
     # k_weight, weight_dtype, freqs, fb, fl, q_out, qo_strides, k_out, ko_strides, v, v_strides, v_out,
     # vo_strides, stream)
