@@ -45,6 +45,7 @@ def _agree(q, s, q_ref, s_ref, code_frac=0.999):
     (300, 3072, 256, torch.float16),
     (129, 2048, 0, torch.bfloat16),
     (64, 8192, 256, torch.float16),
+    (97, 9216, 256, torch.bfloat16),      # 36 groups: one row per 320-thread workgroup
 ])
 def test_gelu_quantize_matches_unfused(gpu, act, M, K, group, dtype):
     g = torch.Generator().manual_seed(M + K)
@@ -108,6 +109,7 @@ def test_int8_mlp_matches_eager(gpu, approximate, bias):
     (4096, 3072, 4096, 256, torch.bfloat16, torch.bfloat16),   # FLUX image stream, one sample
     (2 * 512, 3072, 512, 256, torch.bfloat16, torch.bfloat16), # two samples of text rows
     (333, 2048, 111, 0, torch.float32, torch.float16),          # fp32 residual stream (reference ln_mod)
+    (65, 11264, 65, 256, torch.bfloat16, torch.bfloat16),       # 44 groups: one row per 384-thread workgroup
 ])
 def test_ln_mod_quantize_matches_unfused(gpu, M, K, rpm, group, xdt, mdt):
     """One pass of LayerNorm-modulate + quantize against the reference's

@@ -70,6 +70,9 @@ CONFIG_SHAPES = [
     (65, 15360, 256, torch.float32), (3, 32512, 256, torch.bfloat16), (5, 32768, 0, torch.float16),
     (64, 2304, 0, torch.float16), (50, 2600, 0, torch.bfloat16), (100, 700, 0, torch.float16),
     (4097, 512, 256, torch.bfloat16), (4097, 1024, 0, torch.float16), (1025, 2048, 256, torch.bfloat16),
+    # rows of 36 / 44 / 60 groups (288 / 352 / 480 lanes): one row per workgroup of 320 / 384 / 512
+    # threads instead of two rows in a workgroup above 512 threads
+    (301, 9216, 256, torch.bfloat16), (77, 11264, 0, torch.float16), (1001, 15360, 256, torch.bfloat16),
 ]
 
 
