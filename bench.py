@@ -33,7 +33,8 @@ The same run also measures, and adds to the JSON line:
     python bench.py [--steps K] [--warmup W] [--no-full] [--no-cpu]
     python bench.py --copy-calibration   # 1 GiB device copy for counter scaling
     python bench.py --mfma-ceiling       # MFMA-only throughput (int8, bf16)
-    python bench.py --shapes             # per-shape report for every BASELINE config
+    python bench.py --shapes             # per-shape report for every BASELINE config (+ the GEMM A/B)
+    python bench.py --gemm-ab            # same-process GEMM A/B against torch._int_mm (hipBLASLt)
 """
 
 from __future__ import annotations
@@ -422,6 +423,64 @@ def per_call_ms(fn, reps: int = 20) -> float:
     return t[reps // 2]
 
 
+GEMM_AB_SHAPES = [
+    # FLUX's W8A8 linears: name, M, K, N (bf16 activations and output, bias, ConvRot 256)
+    ("flux_img_qkv", 4096, 3072, 9216),
+    ("flux_img_proj", 4096, 3072, 3072),
+    ("flux_img_mlp_up", 4096, 3072, 12288),
+    ("flux_img_mlp_down", 4096, 12288, 3072),
+    ("flux_single_linear1", 4608, 3072, 21504),
+    ("flux_single_linear2", 4608, 15360, 3072),
+    ("flux_txt_mlp_up", 512, 3072, 12288),
+]
+
+
+def gemm_vendor_ab(dev):
+    """Same process, same ConvRot codes: the reference's ROCm int_mm (torch._int_mm
+    on the transposed weight view, _int8.py:200-207, which runs hipBLASLt) alone
+    and followed by rescale's torch ops (_int8.py:322-323), against this
+    library's int32 GEMM and its fused-epilogue GEMM. One JSON line per shape."""
+    from diffucore_amd import Int8Linear, int_mm, quantize_activation
+    dt = torch.bfloat16
+    g = torch.Generator(device=dev)
+    for name, M, K, N in GEMM_AB_SHAPES:
+        g.manual_seed(0)
+        x = torch.randn(M, K, generator=g, device=dev).to(dt)
+        lin = torch.nn.Linear(K, N, device=dev)
+        lin.weight.normal_(0, 0.02, generator=g)
+        lin.bias.normal_(0, 0.02, generator=g)
+        m = Int8Linear.from_linear(lin, 256)
+        m.bias.data = m.bias.data.to(dt)
+        qx, sx = quantize_activation(x, 256)
+        wt = m.weight.t()
+        sw = m.scale
+
+        def vendor_rescale():
+            acc = torch._int_mm(qx, wt)
+            return (acc.float() * (sx[:, None] * sw[None, :])).to(dt) + m.bias
+
+        ms_v = per_call_ms(lambda: torch._int_mm(qx, wt))
+        ms_vr = per_call_ms(vendor_rescale)
+        ms_i = per_call_ms(lambda: int_mm(qx, m.weight))
+        ms_f = per_call_ms(lambda: m.matmul_quantized(qx, sx, dt))
+        same_acc = bool(torch.equal(torch._int_mm(qx, wt), int_mm(qx, m.weight)))
+        same_out = bool(torch.equal(vendor_rescale(), m.matmul_quantized(qx, sx, dt)))
+        ops = 2 * M * N * K
+
+        def tops(ms):
+            return round(ops / (ms * 1e-3) / 1e12, 1)
+
+        print(json.dumps({"kind": "gemm_vs_vendor", "shape": name, "M": M, "K": K, "N": N,
+                          "plan": __import__("diffucore_amd")._int8.gemm_plan(M, N, K),
+                          "torch_int_mm_ms": round(ms_v, 4), "torch_int_mm_TOPS": tops(ms_v),
+                          "torch_int_mm_rescale_ms": round(ms_vr, 4),
+                          "dc_int32_ms": round(ms_i, 4), "dc_int32_TOPS": tops(ms_i),
+                          "dc_fused_bf16_ms": round(ms_f, 4), "dc_fused_bf16_TOPS": tops(ms_f),
+                          "fused_vs_int_mm": round(ms_v / ms_f, 3),
+                          "int32_equal": same_acc, "fused_equals_int_mm_rescale": same_out}), flush=True)
+        del x, lin, m, qx, sx, wt
+
+
 def _cmp(y, ref):
     a, b = y.float().flatten(), ref.float().flatten()
     return {"max_abs": float((a - b).abs().max()), "rel_l2": float((a - b).norm() / b.norm()),
@@ -624,6 +683,9 @@ def main():
                     help="only run a 1 GiB device copy (scales the rocprofv3 byte counters) and exit")
     ap.add_argument("--shapes", action="store_true",
                     help="only print the per-shape report (every BASELINE config shape) and exit")
+    ap.add_argument("--gemm-ab", action="store_true",
+                    help="only print the same-process GEMM A/B against torch._int_mm (hipBLASLt) at FLUX's "
+                         "linear shapes and exit")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only measure the MFMA-only throughput of the device (int8 and bf16, 1 and 2 waves per "
                          "SIMD, constant and changing operands) and exit")
@@ -645,12 +707,14 @@ def main():
         torch.cuda.set_device(0)
         print(json.dumps({"mfma_ceiling": mfma_ceiling()}), flush=True)
         return
-    if args.shapes:
+    if args.shapes or args.gemm_ab:
         from diffucore_amd import _lib
         _lib.require()
         torch.cuda.set_device(0)
         with torch.no_grad():
-            shapes_report(torch.device("cuda", 0))
+            if args.shapes:
+                shapes_report(torch.device("cuda", 0))
+            gemm_vendor_ab(torch.device("cuda", 0))
         return
 
     import flux_step as FS

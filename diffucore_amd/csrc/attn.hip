@@ -812,6 +812,9 @@ constexpr int WSTAGE = WK_BYTES + WV_BYTES;         // 24 KB
 constexpr int ATTN_WIDE_LDS = ATTN_WIDE_STAGES * WSTAGE;
 constexpr int WIDE_LOADS = 3;                       // DMA instructions per wave per tile: 1 K + 2 V
 constexpr int WIDE_MAX_TILES = 2048;                // K block scales staged in LDS: Lk <= 131072
+// V row strides (elements) below which a tile's 64 V rows span under 2^31
+// bytes, so attn_wide_kernel's 32-bit DMA offsets hold them
+constexpr int64_t WIDE_MAX_VSL = (int64_t)1 << 23;
 
 // vmcnt(n) with the other counters unconstrained (gfx9 encoding: vmcnt bits
 // 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -903,7 +906,7 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
   for (int u = 0; u < 2; ++u) {
     vrow[u] = 4 * (w + 8 * u) + (lane >> 4);
     vcol[u] = min((lane & 15) ^ ((vrow[u] & 3) << 2), p.D / 8 - 1) * 8;
-    voff[u] = (uint32_t)(vrow[u] * (int)p.vsl + vcol[u]) * 2u;   // the host keeps 64 V rows under 2^31 bytes
+    voff[u] = (uint32_t)(vrow[u] * (int)p.vsl + vcol[u]) * 2u;   // the host keeps p.vsl < WIDE_MAX_VSL
   }
   // tile `tile` into stage `st` (tile % STAGES); past the end the source is
   // the last tile again (in bounds; that data is never read)
@@ -1256,7 +1259,13 @@ static int attn_fwd(const void* q, const void* k, const void* v, void* o, int dt
       return DC_EUNSUPPORTED;
     }
   if ((int64_t)Lk + WIN > 0x7fffffff) { set_error("%s: problem too large", who); return DC_EINVAL; }
-  const AttnPlan pl = D <= 64 ? attn_plan_dp<64>(dtype, B, H, Lq, Lk) : attn_plan_dp<128>(dtype, B, H, Lq, Lk);
+  AttnPlan pl = D <= 64 ? attn_plan_dp<64>(dtype, B, H, Lq, Lk) : attn_plan_dp<128>(dtype, B, H, Lq, Lk);
+  if (pl.wide && v_strides[1] >= WIDE_MAX_VSL) {
+    // attn_wide_kernel addresses a tile's 64 V rows with 32-bit offsets; a
+    // longer V row stride takes the 128-query kernel (64-bit offsets) with
+    // whole query tiles, which needs no more workspace than the wide plan
+    pl = AttnPlan{(int)((int64_t)((Lq + BQ - 1) / BQ) * H * B), 0, 0, false};
+  }
   const WsLayout w = ws_layout(B, H, Lk, D, pl.sk_blocks);
   if (!workspace || ws_bytes < w.total) {
     set_error("%s: workspace too small (%zu bytes, this call needs %zu)", who, ws_bytes, w.total);

@@ -1160,6 +1160,10 @@ static int group_setup(const char* who, const dc_gemm_problem* problems, const d
       const dc_gemm_gate& r = gates[i];
       if (!r.res || !r.gate) return group_fail(DC_EINVAL, who, "null residual or gate");
       if (r.ldr < N) return group_fail(DC_EINVAL, who, "ldr < N");
+      // in place, each output element must read only its own residual
+      // element: other row strides would read rows other tiles overwrite
+      if (r.res == q.out && r.ldr != q.ldo)
+        return group_fail(DC_EINVAL, who, "a residual that is the output needs ldr == ldo");
       d.res = r.res; d.gate = r.gate; d.ldr = r.ldr;
       // the residual's loads follow the output's stores, so they need the same alignment
       d.vec_out = d.vec_out && (reinterpret_cast<uintptr_t>(r.res) % (4 * (uintptr_t)ob)) == 0 && r.ldr % 4 == 0;

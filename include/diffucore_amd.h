@@ -318,7 +318,9 @@ int dc_int8_attn_fwd(const void* q, const void* k, const void* v, void* o, int d
  * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
  * (two streams, two threads) race and must be ordered by the caller; calls in
  * one stream are ordered already. Nothing in the scratch needs to start at
- * zero (every byte a call reads, it wrote first).
+ * zero (every byte a call reads, it wrote first). The first call on each
+ * device looks up that device's scratch address (hipGetSymbolAddress): make
+ * one call on a device before capturing calls on it into a HIP graph.
  */
 int dc_int8_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int B,
                              int H, int Lq, int Lk, int D, const int64_t q_strides[3],

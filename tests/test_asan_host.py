@@ -7,9 +7,11 @@ usual and never runs here: the checks return before any launch), then a child
 process with the sanitizer runtime preloaded makes each entry point's invalid
 calls - null pointers, negative or oversized sizes, bad dtypes, misaligned
 pointers and strides, a workspace too small, a call beyond the no-allocation
-scratch - and the valid empty calls that return before any HIP work. Every
-call must return its error code, and any sanitizer report (a non-zero exit,
-or "AddressSanitizer" on stderr) fails the test."""
+scratch, an in-place residual with its own row stride, the MFMA probe's bad
+kinds and counts - and the valid empty calls that return before any HIP work.
+Every call must return its error code, and any sanitizer report (a non-zero
+exit, or "AddressSanitizer" on stderr) fails the test. The sources are the
+library's own list (``diffucore_amd.build.SOURCES``)."""
 
 from __future__ import annotations
 
@@ -23,7 +25,8 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-CSRC = ROOT / "diffucore_amd" / "csrc"
+sys.path.insert(0, str(ROOT))
+from diffucore_amd.build import CSRC, SOURCES  # noqa: E402  (the library's own source list)
 
 
 def _asan_runtime() -> str | None:
@@ -58,11 +61,15 @@ class Gate(ctypes.Structure):
     _fields_ = [("res", P), ("ldr", I64), ("gate", P)]
 ggrp = sig("dc_w8a8_gemm_grouped_gated", I, [P, P, I, I64, I64, I, I, P])
 gplan = sig("dc_w8a8_gemm_group_plan", I, [ctypes.POINTER(I64), I, I64, I64])
+probe = sig("dc_mfma_probe", I, [I, I, I, I, P, P])
 BF16, F16, F32 = 1, 0, 2
 probs = (Prob * 4)(Prob(16, 512, 16, 512, 16, 16, None, 16, 3072, 64), Prob(16, 500, 16, 512, 16, 16, None, 16, 3072, 64),
                    Prob(16, 512, None, 512, 16, 16, None, 16, 3072, 64), Prob(16, 512, 16, 512, 16, 16, None, 16, 3072, 0))
 Ms = (I64 * 4)(4096, 512, 0, 77)
 gates = (Gate * 4)(Gate(16, 3072, 16), Gate(None, 3072, 16), Gate(16, 3000, 16), Gate(None, 0, None))
+# a residual that is the output itself, with a row stride other than the output's
+inplace_p = (Prob * 1)(Prob(16, 512, 16, 512, 16, 16, None, 4096, 3072, 64))
+inplace_g = (Gate * 1)(Gate(4096, 3328, 16))
 st = (I64 * 3)(8, 8, 8)
 bad = (I64 * 3)(8, 12, 8)
 checks = [
@@ -103,6 +110,12 @@ checks = [
     (ggrp(ctypes.byref(probs, 0), ctypes.byref(gates, 2 * ctypes.sizeof(Gate)), 1, 3072, 512, -1, BF16, None), 1),
     (ggrp(ctypes.byref(probs, 3 * ctypes.sizeof(Prob)), ctypes.byref(gates, 3 * ctypes.sizeof(Gate)), 1, 3072, 512,
           -1, BF16, None), 0),
+    (ggrp(inplace_p, inplace_g, 1, 3072, 512, -1, BF16, None), 1),
+    (probe(2, 1, 1, 10, 16, None), 1),
+    (probe(0, 2, 1, 10, 16, None), 1),
+    (probe(0, 1, 3, 10, 16, None), 1),
+    (probe(0, 1, 1, 0, 16, None), 1),
+    (probe(1, 0, 2, 10, None, None), 1),
     (gplan(Ms, 4, 3072, 3072), 1),
     (gplan(Ms, 9, 3072, 3072), -1),
 ]
@@ -128,7 +141,7 @@ def asan_lib(tmp_path_factory):
     out = tmp / "libdiffucore_amd_asan.so"
     flags = ["--offload-arch=gfx950", "-O1", "-g", "-std=c++17", "-fPIC", "-Xarch_host", "-fsanitize=address",
              "-Xarch_host", "-fno-omit-frame-pointer", "-w"]
-    srcs = ("quant.hip", "qknorm.hip", "gemm.hip", "attn.hip", "capi.cpp")
+    srcs = tuple(SOURCES)
     # one compile per source, in parallel, then the link
     procs = [subprocess.Popen([hipcc, *flags, "-c", str(CSRC / s), "-o", str(tmp / f"{s}.o")],
                               stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True) for s in srcs]

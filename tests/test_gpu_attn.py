@@ -262,3 +262,80 @@ def test_stream_k_pieces_match_whole_tiles(gpu):
             sl = slice(t0, t0 + 128)
             assert (a[sl] - b_[sl]).norm() / b_[sl].norm() < 5e-3, (hh, t0)
             assert (a[sl] - ref[sl]).norm() / ref[sl].norm() < 3e-2, (hh, t0)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 128), (torch.bfloat16, 64)])
+def test_null_keys_int8(gpu, dtype, D):
+    """``attention_blhd(..., "int8_turing", null_keys=n)`` (Anima's callers,
+    anima_dit.py:304; reference test_attention_dispatch.py:303-305): the n
+    all-zero key/value rows are padded back before the INT8 kernels run, so
+    the call equals the INT8 call on the padded K/V bit for bit, and stays
+    within the oracle bound on those padded inputs and the reference's SDPA
+    bar."""
+    B, Lq, Lk, H, n = 2, 300, 500, 3, 7
+    q, k, v = _inputs(B, Lq, Lk, H, D, dtype, seed=5)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    out = A.attention_blhd(qd, kd, vd, "int8_turing", null_keys=n)
+    pad = (0, 0, 0, 0, 0, n)
+    kp, vp = F.pad(kd, pad), F.pad(vd, pad)
+    want = A.attention_blhd(qd, kp, vp, "int8_turing")
+    assert torch.equal(out, want)
+    assert not torch.equal(out, A.attention_blhd(qd, kd, vd, "int8_turing"))
+    o = np32(out).reshape(B, Lq, H, D)
+    ora = OA.int8_attention(np32(q), np32(kp), np32(vp), D ** -0.5, DT[dtype], DT[dtype])
+    assert rel_l2(o, ora) < ORACLE_REL[dtype] and cosine(o, ora) > ORACLE_COS
+    ref = np32(_ref_blhd(q.float().to(gpu), kp.float(), vp.float()))
+    assert rel_l2(o, ref) < 3e-2 and cosine(o, ref) > 0.9995
+
+
+@pytest.mark.parametrize("B,H,L,D,dtype", [(2, 10, 4096, 64, torch.float16), (1, 4, 1024, 128, torch.float16)])
+def test_growing_logits_rescale_128_query_kernel(gpu, B, H, L, D, dtype):
+    """The growing-logits case (row maxima rising from ~8 to ~100 over the key
+    range, so the lazy maximum rescales O every few tiles; an unrescaled
+    float16 P would overflow) on the 128-query kernel: at head dim 64 with
+    stream-K pieces and their merge (SDXL's 2 x 10 heads at 4096 tokens), and
+    at head dim 128 on a grid too small for the 256-query kernel. Finite, and
+    within the oracle bound."""
+    pl = A.attn_plan(B, H, L, L, D, dtype)
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert (pl["sk_blocks"] > 0) == (D == 64)
+        assert pl["dp_tiles"] + pl["sk_tiles"] == B * H * L // 128
+    g = torch.Generator().manual_seed(4)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = (8 * u + 0.1 * torch.randn(B, L, H, D, generator=g)).to(dtype)
+    k = (100 * torch.linspace(0, 1, L).view(1, L, 1, 1) * u + torch.randn(B, L, H, D, generator=g)).to(dtype)
+    v = torch.randn(B, L, H, D, generator=g).to(dtype)
+    out, _ = _run(q, k, v, gpu)
+    assert torch.isfinite(out).all()
+    # the last batch's last 4 heads: the query tiles past the whole rounds,
+    # which the stream-K pieces run (the oracle is per (batch, head))
+    sl = (slice(B - 1, B), slice(None), slice(H - 4, H))
+    o = np32(out[sl])
+    ora = OA.int8_attention(np32(q[sl]), np32(k[sl]), np32(v[sl]), D ** -0.5, DT[dtype], DT[dtype])
+    r, c = rel_l2(o, ora), cosine(o, ora)
+    print(f"[attn] growing logits 128-query kernel {B},{H},{L},{D}: vs oracle rel {r:.2e} cos {c:.7f}")
+    assert r < ORACLE_REL[dtype] and c > ORACLE_COS
+
+
+def test_long_v_row_stride_takes_128_query_kernel(gpu):
+    """A V whose row stride puts a 64-key tile past 2^31 bytes (the 256-query
+    kernel's 32-bit DMA offsets) runs the 128-query kernel with whole tiles:
+    same inputs, V laid out with an L-stride of 2^23 elements, against the
+    same V contiguous, within the oracle bound of each other."""
+    B, Lq, Lk, H, D, dtype = 1, 512, 130, 256, 128, torch.bfloat16
+    if A.attn_plan(B, H, Lq, Lk, D, dtype)["dp_tiles"] != B * H * 2:
+        pytest.skip("this grid does not take the 256-query kernel on this device")
+    q, k, v = _inputs(B, Lq, Lk, H, D, dtype, seed=8)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    vsl = 1 << 23
+    store = torch.zeros((Lk - 1) * vsl + H * D, device=gpu, dtype=dtype)
+    vs = store.as_strided((B, Lk, H, D), (Lk * vsl, vsl, D, 1))
+    vs.copy_(vd)
+    ws = torch.empty(A.workspace_bytes(B, H, Lq, Lk, D), device=gpu, dtype=torch.uint8)
+    out = A.int8_attention(qd, kd, vs, D ** -0.5, workspace=ws)
+    base = A.int8_attention(qd, kd, vd, D ** -0.5, workspace=ws)
+    assert np.isfinite(np32(out)).all()
+    assert rel_l2(np32(out), np32(base)) < ORACLE_REL[dtype]
+    ora = OA.int8_attention(np32(q), np32(k), np32(v), D ** -0.5, DT[dtype], DT[dtype])
+    assert rel_l2(np32(out), ora) < ORACLE_REL[dtype] and cosine(np32(out), ora) > ORACLE_COS

@@ -128,3 +128,28 @@ def test_int8_step_is_deterministic(flux):
     v1, lat1 = _run(flux, fused=True)
     v2, lat2 = _run(flux, fused=True)
     assert torch.equal(v1, v2) and torch.equal(lat1, lat2)
+
+
+def test_full_depth_latent_against_bf16(gpu):
+    """BASELINE config 5 at full depth (19 double + 38 single blocks, the
+    bench's seeds): the 4-step schnell latent of the INT8 step (W8A8 block
+    linears, INT8 attention, fused glue) against the bf16 eager step, within
+    rel L2 <= 0.035 and cosine >= 0.9995 (measured 0.025 and 0.9997)."""
+    shape = FS.FluxShape()
+    assert (shape.depth, shape.depth_single) == (19, 38)
+    model = FS.build(shape, gpu, torch.bfloat16, seed=0)
+    x0, txt, y, pe = FS.inputs(shape, gpu)
+    sigmas = FS.schnell_sigmas(4, gpu)
+    with torch.no_grad():
+        lat_bf16 = FS.denoise(model, x0, txt, y, pe, sigmas)
+        quantize_linears(model, FS.block_linear_names(model), gpu, 256)
+        set_attention_backend(model, "int8_turing")
+        set_fused_glue(model, True)
+        lat_int8 = FS.denoise(model, x0, txt, y, pe, sigmas)
+    torch.cuda.synchronize()
+    assert torch.isfinite(lat_int8).all()
+    rl, cl = rel_l2(np32(lat_int8), np32(lat_bf16)), cosine(np32(lat_int8), np32(lat_bf16))
+    print(f"\n[flux step] full depth latent vs bf16: rel_l2 {rl:.4g} cos {cl:.6f}")
+    del model
+    torch.cuda.empty_cache()
+    assert rl <= 0.035 and cl >= 0.9995

@@ -16,10 +16,11 @@ from diffucore_amd import _attention, _lib
 pytestmark = pytest.mark.gpu
 
 
-def _noalloc(q, k, v, sm_scale):
+def _noalloc(q, k, v, sm_scale, out=None):
     so = _lib.require()
     B, Lq, H, D = q.shape
-    out = torch.empty(B, Lq, H, D, device=q.device, dtype=q.dtype)
+    if out is None:
+        out = torch.empty(B, Lq, H, D, device=q.device, dtype=q.dtype)
     with torch.cuda.device(q.device):
         rc = so.dc_int8_attn_fwd_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                          _lib.dtype_code(q.dtype), B, H, Lq, k.shape[1], D,
@@ -73,3 +74,36 @@ def test_noalloc_rejects_calls_beyond_its_scratch(gpu):
     rc = so.dc_int8_attn_fwd_noalloc(16, 16, 16, 16, _lib.BF16, B, H, L, L, D, st, st, st, st,
                                      ctypes.c_float(0.1), None)
     assert rc == 4 and b"scratch" in so.dc_last_error()
+
+
+def test_noalloc_graph_replays(gpu):
+    """Captured in a HIP graph after one eager call on the device (which looks
+    up the scratch array's address; the header asks for that call before any
+    capture), then replayed three times between eager calls of other shapes
+    that overwrite the scratch: each replay equals the eager bits, and new
+    values in the captured inputs reach the next replay."""
+    q, k, v = _qkv(2, 10, 1024, 1024, 64, torch.float16, gpu, seed=21)
+    want = _attention.int8_attention(q, k, v, 0.125)
+    out = _noalloc(q, k, v, 0.125)
+    assert torch.equal(out, want)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _noalloc(q, k, v, 0.125, out)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _noalloc(q, k, v, 0.125, out)
+    for rep in range(3):
+        other = _qkv(1, 24, 700, 900, 128, torch.bfloat16, gpu, seed=30 + rep)
+        _noalloc(*other, 128 ** -0.5)
+        torch.cuda.synchronize()
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+    k.add_(1.0)
+    want2 = _attention.int8_attention(q, k, v, 0.125)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want2) and not torch.equal(out, want)
