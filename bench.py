@@ -439,7 +439,9 @@ def gemm_vendor_ab(dev):
     """Same process, same ConvRot codes: the reference's ROCm int_mm (torch._int_mm
     on the transposed weight view, _int8.py:200-207, which runs hipBLASLt) alone
     and followed by rescale's torch ops (_int8.py:322-323), against this
-    library's int32 GEMM and its fused-epilogue GEMM. One JSON line per shape."""
+    library's int32 GEMM and its fused-epilogue GEMM, each timed as GPU time
+    per call over a captured graph of back-to-back calls. One JSON line per
+    shape."""
     from diffucore_amd import Int8Linear, int_mm, quantize_activation
     dt = torch.bfloat16
     g = torch.Generator(device=dev)
@@ -459,10 +461,10 @@ def gemm_vendor_ab(dev):
             acc = torch._int_mm(qx, wt)
             return (acc.float() * (sx[:, None] * sw[None, :])).to(dt) + m.bias
 
-        ms_v = per_call_ms(lambda: torch._int_mm(qx, wt))
-        ms_vr = per_call_ms(vendor_rescale)
-        ms_i = per_call_ms(lambda: int_mm(qx, m.weight))
-        ms_f = per_call_ms(lambda: m.matmul_quantized(qx, sx, dt))
+        ms_v = graph_call_ms(lambda: torch._int_mm(qx, wt))
+        ms_vr = graph_call_ms(vendor_rescale)
+        ms_i = graph_call_ms(lambda: int_mm(qx, m.weight))
+        ms_f = graph_call_ms(lambda: m.matmul_quantized(qx, sx, dt))
         same_acc = bool(torch.equal(torch._int_mm(qx, wt), int_mm(qx, m.weight)))
         same_out = bool(torch.equal(vendor_rescale(), m.matmul_quantized(qx, sx, dt)))
         ops = 2 * M * N * K
@@ -479,6 +481,34 @@ def gemm_vendor_ab(dev):
                           "fused_vs_int_mm": round(ms_v / ms_f, 3),
                           "int32_equal": same_acc, "fused_equals_int_mm_rescale": same_out}), flush=True)
         del x, lin, m, qx, sx, wt
+
+
+def graph_call_ms(fn, reps: int = 20) -> float:
+    """GPU time per call of ``fn`` with no host launch cost: ``reps`` back-to-back
+    calls captured in one HIP graph, the median of 7 replays divided by
+    ``reps`` (a call's launches, and the gaps between them, included)."""
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(7):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / reps)
+    return sorted(ts)[3]
 
 
 def _cmp(y, ref):
@@ -504,6 +534,7 @@ def shapes_report(dev):
         k = k.to(dt).reshape(B, Skv, H * D).view(B, Skv, H, D).transpose(1, 2)
         v = torch.randn(B, Skv, H * D, generator=g, device=dev).to(dt).view(B, Skv, H, D).transpose(1, 2)
         ms = per_call_ms(lambda: attention_bhld(q, k, v, "int8_turing"))
+        ms_gpu = graph_call_ms(lambda: attention_bhld(q, k, v, "int8_turing"))
         ms_sdpa = per_call_ms(lambda: F.scaled_dot_product_attention(q, k, v))
         # the reference's SDPA backend with the same (B, Sq, H*D) output
         ms_sdpa_path = per_call_ms(lambda: attention_bhld(q, k, v, "sdpa"))
@@ -511,9 +542,10 @@ def shapes_report(dev):
         route = "sdpa (short key range)" if Skv <= SHORT_KEYS else "int8"
         ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(B, S, H * D)
         ops = 4 * B * H * S * Skv * D
-        tops = ops / (ms * 1e-3) / 1e12
+        tops = ops / (ms_gpu * 1e-3) / 1e12
         print(json.dumps({"kind": "attention", "shape": name, "B": B, "H": H, "Sq": S, "Skv": Skv, "D": D,
-                          "dtype": str(dt)[6:], "ms": round(ms, 4), "TOPS": round(tops, 1),
+                          "dtype": str(dt)[6:], "ms": round(ms, 4), "gpu_ms": round(ms_gpu, 4),
+                          "TOPS": round(tops, 1),
                           "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
                           "pct_mixed_ceiling": round(100 * tops / mixed_peak, 2),
                           "sdpa_ms": round(ms_sdpa, 4), "sdpa_backend_ms": round(ms_sdpa_path, 4), "route": route,
@@ -537,6 +569,9 @@ def shapes_report(dev):
         ms_q = per_call_ms(lambda: quantize_activation(x, group))
         qx, sx = quantize_activation(x, group)
         ms_g = per_call_ms(lambda: m.matmul_quantized(qx, sx, dt))
+        # GPU time alone (no host launch cost), for the rates and % of HBM
+        ms_qg = graph_call_ms(lambda: quantize_activation(x, group))
+        ms_gg = graph_call_ms(lambda: m.matmul_quantized(qx, sx, dt))
         y = m.matmul_quantized(qx, sx, dt)
         # the reference's unfused int8 path on the same codes: exact int32 sums
         # (float64 holds them), then rescale's torch ops (_int8.py:322-323)
@@ -546,12 +581,18 @@ def shapes_report(dev):
         yf = F.linear(x.float(), lin.weight.float(), lin.bias.float())
         ops = 2 * M * N * K
         qbytes = M * K * x.element_size() + M * K + 4 * M
-        tops = ops / (ms_g * 1e-3) / 1e12
+        # the GEMM's algorithmic bytes: int8 operands, scales, bias, output
+        gbytes = M * K + N * K + 4 * (M + N) + N * m.bias.element_size() + M * N * x.element_size()
+        tops = ops / (ms_gg * 1e-3) / 1e12
         print(json.dumps({"kind": "w8a8_linear", "shape": name, "M": M, "K": K, "N": N, "group": group,
-                          "dtype": str(dt)[6:], "gemm_ms": round(ms_g, 4), "TOPS": round(tops, 1),
+                          "dtype": str(dt)[6:], "plan": __import__("diffucore_amd")._int8.gemm_plan(M, N, K),
+                          "gemm_ms": round(ms_g, 4), "gemm_gpu_ms": round(ms_gg, 4), "TOPS": round(tops, 1),
                           "pct_int8_peak": round(100 * tops / INT8_PEAK_TOPS, 2),
-                          "quant_ms": round(ms_q, 4), "quant_GBps": round(qbytes / (ms_q * 1e-3) / 1e9, 1),
-                          "quant_pct_hbm": round(100 * qbytes / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                          "gemm_bytes": gbytes, "gemm_GBps": round(gbytes / (ms_gg * 1e-3) / 1e9, 1),
+                          "gemm_pct_hbm": round(100 * gbytes / (ms_gg * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                          "quant_ms": round(ms_q, 4), "quant_gpu_ms": round(ms_qg, 4),
+                          "quant_GBps": round(qbytes / (ms_qg * 1e-3) / 1e9, 1),
+                          "quant_pct_hbm": round(100 * qbytes / (ms_qg * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
                           "vs_int_mm_rescale": _cmp(y, ref), "vs_float_linear": _cmp(y, yf)}), flush=True)
         del x, lin, m, qx, sx, y, acc, ref, yf
     # UNet self-attention q/k/v: separate layers, one shared quantization (the

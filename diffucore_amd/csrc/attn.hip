@@ -87,11 +87,18 @@ __device__ __forceinline__ void unpack8(uint4 u, float (&f)[8]) {
   }
 }
 
+// Four codes rint(f[i] * inv) as bytes of one word. The product is rounded
+// to float32 first; adding 1.5 * 2^23 then rounds it to an integer n, ties to
+// even, exactly as rintf does (|product| < 2^22: the codes are within
+// +-128), and leaves the bits 0x4B400000 + n, whose low byte is n as an int8.
+// Two byte permutes and an or gather the four low bytes.
 __device__ __forceinline__ uint32_t pack_codes(const float* f, float inv) {
-  uint32_t r = 0;
+  uint32_t b[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r |= (uint32_t)(uint8_t)(int8_t)(int)rintf(f[i] * inv) << (8 * i);
-  return r;
+  for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(materialize(f[i] * inv) + MAGIC_F);
+  // v_perm_b32 selector bytes: 0..3 pick bytes of the second operand, 4..7
+  // of the first, 0x0c gives 0
+  return __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);
 }
 
 // ---------------------------------------------------------------- 1. key sums
@@ -120,40 +127,61 @@ __global__ void __launch_bounds__(256) kstats_kernel(AttnArgs p) {
       for (int e = 0; e < 8; ++e) ak[e] += f[e];   // + 0 leaves a sum that started at +0 unchanged
     }
   }
-  __shared__ float red[16][129];
+  // The 16 row groups' partial sums, then each channel's 16 partials added in
+  // row-group order. Row group rg keeps channels 8 ch + 0..3 at float
+  // 4 ch + 0..3 and 8 ch + 4..7 at 96 + 4 ch + 0..3 of its 160-float row: the
+  // 16 lanes of one row group write 256 contiguous bytes per half, and the 64
+  // channels a wave reads fall in distinct banks, so neither side conflicts.
+  __shared__ __attribute__((aligned(16))) float red[16 * 160];
   if (ch * 8 < p.D) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) red[rg][ch * 8 + i] = ak[i];
+    *reinterpret_cast<float4*>(red + rg * 160 + 4 * ch) = make_float4(ak[0], ak[1], ak[2], ak[3]);
+    *reinterpret_cast<float4*>(red + rg * 160 + 96 + 4 * ch) = make_float4(ak[4], ak[5], ak[6], ak[7]);
   }
   __syncthreads();
   if (t < p.D) {
+    const int idx = ((t & 4) ? 96 : 0) + 4 * (t >> 3) + (t & 3);
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s += red[i][t];
+    for (int i = 0; i < 16; ++i) s += red[i * 160 + idx];
     p.kpart[((int64_t)(b * p.H + h) * p.nwin + w) * p.D + t] = s;
   }
 }
 
 // ---------------------------------------------------------------- 2. K quantize
 
+// 64-key blocks per kquant workgroup: one per wave, so a block's absmax is a
+// wave reduction and the window sum is read once per KQ_BLOCKS blocks
+constexpr int KQ_BLOCKS = 4;
+
+// A workgroup takes blocks KQ_BLOCKS g .. + 3 of one (b, h), wave wv block
+// KQ_BLOCKS g + wv. Lane l covers channels 16 cp .. 16 cp + 15 (cp = l % LPR)
+// of key rows l / LPR + RPP j: two 16-byte loads and one 16-byte store of
+// codes per row.
 template <int DT, int DP>
 __global__ void __launch_bounds__(256) kquant_kernel(AttnArgs p) {
-  constexpr int CPR = DP / 8;            // 8-channel chunks per key row
-  constexpr int NU = BKEY * CPR / 256;   // chunks per thread
-  const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int bh = b * p.H + h, t = threadIdx.x;
-  __shared__ float ksum_s[128];
-  __shared__ float red[4];
+  constexpr int LPR = DP / 16;          // lanes per key row
+  constexpr int RPP = 64 / LPR;         // rows per pass of the wave
+  constexpr int NP = BKEY / RPP;        // passes over the block
+  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int bh = b * p.H + h, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int nblk = p.Lk64 / BKEY;
+  const int blk = KQ_BLOCKS * g + wv;
+  __shared__ __attribute__((aligned(16))) float ksum_s[128];
 
-  // the tile's key loads first (clamped in bounds, used after the window sums
-  // below), so they are in flight while the sums are read and added
+  // the block's key loads first (clamped in bounds: a wave past the last
+  // block reads it again, rows past Lk read row Lk - 1, chunks past D the last
+  // chunk inside D; none of those values is used), so they are in flight
+  // while the window sums are read and added
+  const int cp = lane % LPR, r0 = lane / LPR;
+  const int c0 = min(2 * cp, p.D / 8 - 1), c1 = min(2 * cp + 1, p.D / 8 - 1);
   const uint16_t* kb = static_cast<const uint16_t*>(p.k) + b * p.ksb + h * p.ksh;
-  uint4 raw[NU];
+  const int k0 = min(blk, nblk - 1) * BKEY;
+  uint4 raw[NP][2];
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    const int ci = t + u * 256, r = ci / CPR, c = ci % CPR;
-    const int row = min(tile * BKEY + r, p.Lk - 1), cc = min(c, p.D / 8 - 1);
-    raw[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)row * p.ksl + cc * 8);
+  for (int j = 0; j < NP; ++j) {
+    const int64_t row = min(k0 + r0 + RPP * j, p.Lk - 1) * p.ksl;
+    raw[j][0] = *reinterpret_cast<const uint4*>(kb + row + c0 * 8);
+    raw[j][1] = *reinterpret_cast<const uint4*>(kb + row + c1 * 8);
   }
 
   if (t < p.D) {
@@ -169,39 +197,47 @@ __global__ void __launch_bounds__(256) kquant_kernel(AttnArgs p) {
         if (w0 + i < p.nwin) s += part[i];
     }
     ksum_s[t] = s;
-    if (tile == 0) p.ksum[(int64_t)bh * p.D + t] = s;
+    if (g == 0) p.ksum[(int64_t)bh * p.D + t] = s;
   }
   __syncthreads();
+  if (blk >= nblk) return;
 
+  // the lane's 16 channel sums (channels past D: 0, their values are zeroed)
+  const bool in0 = 16 * cp < p.D, in1 = 16 * cp + 8 < p.D;
+  float km[16];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const bool in = hh ? in1 : in0;
+    const float4 a = in ? *reinterpret_cast<const float4*>(ksum_s + 16 * cp + 8 * hh) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 c = in ? *reinterpret_cast<const float4*>(ksum_s + 16 * cp + 8 * hh + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    km[8 * hh] = a.x; km[8 * hh + 1] = a.y; km[8 * hh + 2] = a.z; km[8 * hh + 3] = a.w;
+    km[8 * hh + 4] = c.x; km[8 * hh + 5] = c.y; km[8 * hh + 6] = c.z; km[8 * hh + 7] = c.w;
+  }
   const float inv_l = 1.f / (float)p.Lk;
-  float val[NU][8];
+  float val[NP][16];
   float amax = 0.f;
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    const int ci = t + u * 256, r = ci / CPR, c = ci % CPR;
-    if (tile * BKEY + r < p.Lk && c * 8 < p.D) {
+  for (int j = 0; j < NP; ++j) {
+    const bool rin = k0 + r0 + RPP * j < p.Lk;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
       float f[8];
-      unpack8<DT>(raw[u], f);
+      unpack8<DT>(raw[j][hh], f);
+      const bool in = rin && (hh ? in1 : in0);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) val[u][i] = __builtin_fmaf(-ksum_s[c * 8 + i], inv_l, f[i]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) val[u][i] = 0.f;
+      for (int i = 0; i < 8; ++i) val[j][8 * hh + i] = in ? __builtin_fmaf(-km[8 * hh + i], inv_l, f[i]) : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(val[u][i]));
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(val[j][i]));
   }
   amax = wave_max(amax);
-  if ((t & 63) == 0) red[t >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float inv = amax > 0.f ? 127.f / amax : 0.f;
-  if (t == 0) p.ks[(int64_t)bh * (p.Lk64 / BKEY) + tile] = amax / 127.f;
+  if (lane == 0) p.ks[(int64_t)bh * nblk + blk] = amax / 127.f;
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    const int ci = t + u * 256, r = ci / CPR, c = ci % CPR;
-    int8_t* dst = p.k8 + ((int64_t)bh * p.Lk64 + tile * BKEY + r) * DP + c * 8;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_codes(val[u], inv), pack_codes(val[u] + 4, inv));
+  for (int j = 0; j < NP; ++j) {
+    int8_t* dst = p.k8 + ((int64_t)bh * p.Lk64 + k0 + r0 + RPP * j) * DP + 16 * cp;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(pack_codes(val[j], inv), pack_codes(val[j] + 4, inv),
+                                                pack_codes(val[j] + 8, inv), pack_codes(val[j] + 12, inv));
   }
 }
 
@@ -1181,7 +1217,8 @@ template <int DT, int DP>
 static int launch_attn(AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((kstats_kernel<DT>), dim3(a.nwin, a.H, a.B), dim3(256), 0, st, a);
   if (int e = launch_status("kstats_kernel")) return e;
-  hipLaunchKernelGGL((kquant_kernel<DT, DP>), dim3(a.Lk64 / BKEY, a.H, a.B), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((kquant_kernel<DT, DP>), dim3((a.Lk64 / BKEY + KQ_BLOCKS - 1) / KQ_BLOCKS, a.H, a.B), dim3(256),
+                     0, st, a);
   if (int e = launch_status("kquant_kernel")) return e;
   if constexpr (DP == 128) {
     if (a.wide) {

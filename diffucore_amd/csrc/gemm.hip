@@ -88,6 +88,18 @@ __device__ __forceinline__ float load_bias(const void* b, int n) {
   else return h16_to_f32<BIAS_DT>(static_cast<const uint16_t*>(b)[n]);
 }
 
+// A float32 / 16-bit float element as its bits, and back to a float.
+template <int DT>
+__device__ __forceinline__ uint32_t raw_bits(const void* b, int n) {
+  if constexpr (DT == DC_F32) return __float_as_uint(static_cast<const float*>(b)[n]);
+  else return static_cast<const uint16_t*>(b)[n];
+}
+template <int DT>
+__device__ __forceinline__ float from_bits(uint32_t v) {
+  if constexpr (DT == DC_F32) return __uint_as_float(v);
+  else return h16_to_f32<DT>(v);
+}
+
 template <int OUT_DT, int BIAS_DT>
 __device__ __forceinline__ float epi(int acc, float sxm, float swn, const void* bias, int n) {
   float y = round_to<OUT_DT>(materialize((float)acc * (sxm * swn)));
@@ -313,23 +325,50 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[FN][FM], const Gemm
     }
 }
 
-// This tile's output-channel scales, biases (rounded to the output dtype),
-// gate values (RES) and row scales into LDS for the epilogue (threads
-// t = 0 .. nt - 1).
-template <int OUT_DT, int BIAS_DT, bool RES = false>
-__device__ __forceinline__ void stage_epilogue_vectors(const GemmArgs& p, int m0, int n0, int BM, int BN, int t,
-                                                       int nt, float* sw_l, float* b_l, float* sx_l,
-                                                       float* g_l = nullptr) {
-  if constexpr (OUT_DT != DC_I32) {
-    for (int i = t; i < BN; i += nt) {
-      const int n = min(n0 + i, p.N - 1);
-      sw_l[i] = p.sw[n];
-      if constexpr (BIAS_DT != DC_NONE) b_l[i] = round_to<OUT_DT>(load_bias<BIAS_DT>(p.bias, n));
-      if constexpr (RES) g_l[i] = load_bias<OUT_DT>(p.gate, n);   // the gate is of the output dtype
+// This tile's epilogue vectors for thread t: output-channel scale, bias
+// and gate (RES) of channel n0 + t (t < BN) and row scale of row m0 + t
+// (t < BM), as loaded (16-bit values as their bits). Every tile shape has
+// BN, BM <= its thread count, so one entry per thread covers them. They are
+// loaded at the start of the tile, before its operand loads, and written to
+// LDS (EpiRegs::stage) only once those have been waited for, so their memory
+// latency runs under the operand loads' instead of ahead of it.
+struct EpiRegs {
+  uint32_t sw, b, sx, g;
+
+  template <int OUT_DT, int BIAS_DT, bool RES = false>
+  __device__ __forceinline__ static EpiRegs load(const GemmArgs& p, int m0, int n0, int BM, int BN, int t) {
+    EpiRegs r{0u, 0u, 0u, 0u};
+    if constexpr (OUT_DT != DC_I32) {
+      const int n = min(n0 + t, p.N - 1);
+      if (t < BN) {
+        r.sw = __float_as_uint(p.sw[n]);
+        if constexpr (BIAS_DT != DC_NONE) r.b = raw_bits<BIAS_DT>(p.bias, n);
+        if constexpr (RES) r.g = raw_bits<OUT_DT>(p.gate, n);   // the gate is of the output dtype
+      }
+      if (t < BM) r.sx = __float_as_uint(p.sx[min(m0 + t, p.M - 1)]);
     }
-    for (int i = t; i < BM; i += nt) sx_l[i] = p.sx[min(m0 + i, p.M - 1)];
+    return r;
   }
-}
+
+  // Into the tile's LDS vectors: scales as loaded, the bias rounded to the
+  // output dtype, the gate as a float.
+  // The values pass an empty asm here first: without it the compiler moves
+  // the bias rounding up to the load and waits for the load there.
+  template <int OUT_DT, int BIAS_DT, bool RES = false>
+  __device__ __forceinline__ void stage(int BM, int BN, int t, float* sw_l, float* b_l, float* sx_l,
+                                        float* g_l = nullptr) const {
+    if constexpr (OUT_DT != DC_I32) {
+      uint32_t vsw = sw, vb = b, vsx = sx, vg = g;
+      asm volatile("" : "+v"(vsw), "+v"(vb), "+v"(vsx), "+v"(vg));
+      if (t < BN) {
+        sw_l[t] = __uint_as_float(vsw);
+        if constexpr (BIAS_DT != DC_NONE) b_l[t] = round_to<OUT_DT>(from_bits<BIAS_DT>(vb));
+        if constexpr (RES) g_l[t] = from_bits<OUT_DT>(vg);
+      }
+      if (t < BM) sx_l[t] = __uint_as_float(vsx);
+    }
+  }
+};
 
 // Epilogue of one wave's full 128 (n) x 128 (m) block through LDS: the output
 // values go to the wave's own 32 KB of LDS (`stage`, free after the main
@@ -542,9 +581,10 @@ __global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
   float* sw_l = reinterpret_cast<float*>(smem + 2 * STAGE);
   float* b_l = sw_l + BN;
   float* sx_l = b_l + BN;
-  stage_epilogue_vectors<OUT_DT, BIAS_DT>(p, m0, n0, BM, BN, t, NT, sw_l, b_l, sx_l);
+  const EpiRegs ev = EpiRegs::load<OUT_DT, BIAS_DT>(p, m0, n0, BM, BN, t);
   GEMM_LOAD(0, 0);
   GEMM_STORE(0, 0, 0);
+  ev.stage<OUT_DT, BIAS_DT>(BM, BN, t, sw_l, b_l, sx_l);   // loaded before tile 0, so already here
   static_for<T::RB>([&](auto i_) {
     constexpr int i = decltype(i_)::value + 1;
     GEMM_LOAD(i % T::RB, i);
@@ -651,8 +691,8 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p, Group
   float* b_l = epi_v + BN;
   float* sx_l = epi_v + 2 * BN;
   float* g_l = RES ? epi_v + 2 * BN + BM : nullptr;
-  stage_epilogue_vectors<OUT_DT, BIAS_DT, RES>(p, m0, n0, BM, BN, t, 256, sw_l, b_l, sx_l, g_l);
-  __syncthreads();
+  // issued ahead of the operand loads; staged in LDS after the main loop
+  const EpiRegs ev = EpiRegs::load<OUT_DT, BIAS_DT, RES>(p, m0, n0, BM, BN, t);
 
   // DMA sources: wave w loads 1 KB blocks j = w + 4 u (rows 16 j .. 16 j + 15)
   // of W and of A; lane i covers row 16 j + i / 4, logical chunk
@@ -759,9 +799,10 @@ __global__ void __launch_bounds__(256, 1) w8a8_gemm_dma_kernel(GemmArgs p, Group
 #undef DMA_STAGE
   // no load may still be writing this workgroup's LDS when it ends
   DC_WAIT_VMCNT(0);
+  ev.stage<OUT_DT, BIAS_DT, RES>(BM, BN, t, sw_l, b_l, sx_l, g_l);
+  __syncthreads();   // the epilogue vectors are in LDS; every wave is done reading the stage buffers
 
   if (p.vec16 && m0 + BM <= p.M && n0 + BN <= p.N) {
-    __syncthreads();   // every wave is done reading the stage buffers
     uint8_t* stg = w == 0 ? st0 : (w == 1 ? st1 : (w == 2 ? st2 : st3));
     store_tile_lds<OUT_DT, BIAS_DT, RES>(acc, p, m0, n0, wn * 128, wm * 128, sw_l, b_l, sx_l, hf, l32, lane, stg,
                                          g_l);
@@ -888,24 +929,30 @@ static int device_cus() {
   return n;
 }
 
-// Tile shape by the fraction of the device the last round of tiles keeps busy,
-// weighted by each shape's per-tile efficiency (measured): 256 x 256 (the
-// DMA-fed 4-wave kernel when K % 256 == 0, else 8 waves; 1 per CU),
+// Tile shape by the share of the device's tile slots, over the rounds the
+// problem takes, that hold useful work (the output area M x N over all the
+// slot-tiles of those rounds, so a tile's padding past M or N counts as
+// waste), weighted by each shape's per-tile efficiency (measured): 256 x 256
+// (the DMA-fed 4-wave kernel when K % 256 == 0, else 8 waves; 1 per CU),
 // 192 (n) x 256 (m) on 8 waves (1 per CU, wave tiles 96 x 64), 128 x 128 on
 // 4 waves (2 per CU). A 4096 x 9216 problem, say, is 576 tiles of
-// 256 x 256 (2.25 rounds on 256 CUs) but exactly 768 of 192 x 256.
+// 256 x 256 (2.25 rounds on 256 CUs) but exactly 768 of 192 x 256. The
+// 128 x 128 tiles lose less to their prologue and epilogue the shorter K is:
+// measured on the SD1.5 / SDXL / FLUX shapes, they match or beat the larger
+// tiles at equal fill below K = 3072 (0.9) and reach 0.7 of them beyond.
 // Kernel plan for a problem: DC_GEMM_PLAN_* (the choice pick_tile launches).
 static int plan_tile(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
   struct Cand { int bn, bm, per_cu; float eff; };
-  constexpr Cand cands[3] = {{256, 256, 1, 1.0f}, {192, 256, 1, 0.95f}, {128, 128, 2, 0.7f}};
+  const Cand cands[3] = {{256, 256, 1, 1.0f}, {192, 256, 1, 0.95f}, {128, 128, 2, K < 3072 ? 0.9f : 0.7f}};
   const int cus = device_cus();
   int best = 0;
   float best_score = -1.0f;
   for (int i = 0; i < 3; ++i) {
-    const int64_t tiles = ((N + cands[i].bn - 1) / cands[i].bn) * ((M + cands[i].bm - 1) / cands[i].bm);
+    const int64_t tn = (N + cands[i].bn - 1) / cands[i].bn, tm = (M + cands[i].bm - 1) / cands[i].bm;
     const int64_t slots = (int64_t)cus * cands[i].per_cu;
-    const int64_t rounds = (tiles + slots - 1) / slots;
-    const float score = (float)tiles / (float)(rounds * slots) * cands[i].eff;
+    const int64_t rounds = (tn * tm + slots - 1) / slots;
+    const double area = (double)rounds * slots * cands[i].bn * cands[i].bm;
+    const float score = (float)((double)M * (double)N / area) * cands[i].eff;
     if (score > best_score) best = i, best_score = score;
   }
   if (best == 0) {
