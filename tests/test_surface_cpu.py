@@ -169,14 +169,55 @@ def test_group_must_divide_in_features():
         D.Int8Linear(320, 64, group=256)
 
 
-def test_hot_path_has_no_cpu_fallback():
-    m = D.Int8Linear.from_linear(nn.Linear(256, 32))
-    with pytest.raises(RuntimeError, match="GPU only"):
-        m(torch.randn(3, 256))
-    with pytest.raises(RuntimeError, match="GPU only"):
-        D.quantize_activation(torch.randn(3, 256), 256)
+@pytest.mark.parametrize("group,dtype,bias", [(256, torch.float32, True), (0, torch.float32, False),
+                                              (256, torch.bfloat16, True), (0, torch.float16, True)])
+def test_w8a8_on_cpu_tensors_is_the_reference_torch_path(group, dtype, bias):
+    """CPU tensors run the reference's own torch statement of the W8A8 path
+    (``_int8.py:200-207, 299-323``): rotate + per-row int8, ``torch._int_mm``
+    (M <= 16 padded to 32), rescale. Codes, scales and outputs equal the
+    oracle's CPU restatement of that path bit for bit, at M below and above
+    the padding threshold; ``scaled_mm`` keeps its None answer on the CPU."""
+    from oracle import cpu_path as CP
+    torch.manual_seed(3)
+    lin = nn.Linear(512, 96, bias=bias).to(dtype)
+    m = D.Int8Linear.from_linear(lin, group)
+    for rows in (5, 40):
+        x = torch.randn(rows, 512).to(dtype)
+        q, s = D.quantize_activation(x, group)
+        q_ref, s_ref = CP.quantize_rows(CP.rotate(x.float(), group))
+        assert torch.equal(q, q_ref) and torch.equal(s, s_ref)
+        acc = D.int_mm(q, m.weight)
+        assert acc.dtype == torch.int32 and torch.equal(acc, q.long().matmul(m.weight.long().T).int())
+        y = m(x)
+        want = CP.rescale(CP.int_mm(q_ref, m.weight), s_ref, m.scale, m.bias, dtype)
+        assert y.dtype == dtype and torch.equal(y, want)
+        ys = D.linear_group([m, m], [x, x])
+        assert all(torch.equal(t, y) for t in ys)
     assert D.scaled_mm(torch.zeros(3, 16, dtype=torch.int8), torch.zeros(8, 16, dtype=torch.int8),
                        torch.ones(3), torch.ones(8), torch.float16) is None
+
+
+def test_device_tensors_never_take_the_torch_path(monkeypatch):
+    """The torch statement is only for CPU tensors: any other tensor goes to
+    the HIP library, and with the library missing the call raises instead of
+    running the torch ops (no silent fallback). A meta tensor stands in for a
+    GPU tensor, with the GPU-device check disabled and the library made to
+    look missing."""
+    from diffucore_amd import _int8, _lib
+
+    def missing():
+        raise RuntimeError("libdiffucore_amd.so is not built")
+
+    monkeypatch.setattr(_lib, "require", missing)
+    monkeypatch.setattr(_int8, "_on_gpu", lambda t, what: None)
+    x = torch.empty(4, 256, device="meta")
+    q8 = torch.empty(4, 256, dtype=torch.int8, device="meta")
+    for call in (lambda: _int8.quantize_activation(x, 256), lambda: _int8.int_mm(q8, q8),
+                 lambda: _int8.rescale(torch.empty(4, 8, dtype=torch.int32, device="meta"),
+                                       torch.empty(4, device="meta"), torch.empty(8, device="meta"), None,
+                                       torch.float16)):
+        with pytest.raises(RuntimeError, match="not built"):
+            call()
 
 
 def test_entry_points_refuse_host_tensors_before_any_launch():
@@ -193,8 +234,7 @@ def test_entry_points_refuse_host_tensors_before_any_launch():
         A.int8_attention(q, q, q, 0.125)
     with pytest.raises(RuntimeError, match="GPU tensors"):
         A.quantize_q(q)
-    with pytest.raises(RuntimeError, match="GPU only"):
-        D.rescale(torch.zeros(3, 8, dtype=torch.int32), torch.ones(3), torch.ones(8), None, torch.float16)
+
 
 
 def test_quantize_and_dequantize_linears():
