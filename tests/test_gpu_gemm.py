@@ -407,3 +407,64 @@ def test_matmul_quantized_gated_layers(gpu):
     q2 = _int8.quantize_activation(x2.reshape(-1, 3072), 256)
     (y3,) = _int8.matmul_quantized_gated([(la, *q2, r2, g2)], bf)
     assert torch.equal(y3.view(r2.shape), r2 + g2 * la(x2))
+
+
+# Problems of whole 256 x 256 tiles with 16-bit outputs that take several
+# rounds of DMA-fed workgroups, whole and ragged: 992 tiles end on a short
+# round, 756 leave 12 CUs one tile fewer; 768 tiles of K = 3072 are FLUX's
+# image MLP up.
+MULTI_ROUND = [(4096, 15872, 512), (2304, 21504, 512), (4096, 12288, 3072)]
+
+
+def _int32_then_rescale(q, w, sx, sw, bias, dtype):
+    """The same GEMM as an int32 product followed by dc_rescale: the fused
+    epilogue's contract (reference ``_int8.py:313-323``)."""
+    return _int8.rescale(_int8.int_mm(q, w), sx, sw, bias, dtype)
+
+
+@pytest.mark.parametrize("mnk", MULTI_ROUND)
+@pytest.mark.parametrize("dtype,bias_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, None),
+                                              (torch.float16, torch.float32)])
+def test_multi_round_gemm_bit_exact(gpu, mnk, dtype, bias_dtype):
+    """Several rounds of 256 x 256 tiles: bit for bit the int32 product +
+    rescale, the first rows the oracle, and the same bits on every call."""
+    m, n, k = mnk
+    q, w, sx, sw = _qw(m, n, k, 21)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(21)) * 0.5).to(bias_dtype) \
+        if bias_dtype is not None else None
+    rows = 96   # a slice of rows against the oracle (the whole product is minutes of CPU)
+    ref = OG.rescale(OG.int_mm(q[:rows].numpy(), w.numpy()), sx[:rows].numpy(), sw.numpy(),
+                     np32(bias) if bias is not None else None, DT[dtype])
+    q, w, sx, sw = q.to(gpu), w.to(gpu), sx.to(gpu), sw.to(gpu)
+    bias = bias.to(gpu) if bias is not None else None
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert _int8.gemm_plan(m, n, k) == "dma_256x256"
+    y = _gemm_unsplit(q, w, sx, sw, bias, dtype)
+    assert np.array_equal(np32(y[:rows]).view(np.uint32), ref.view(np.uint32))
+    assert torch.equal(y, _int32_then_rescale(q, w, sx, sw, bias, dtype))
+    for _ in range(3):
+        assert torch.equal(_gemm_unsplit(q, w, sx, sw, bias, dtype), y)
+
+
+@pytest.mark.parametrize("ms,n,k,dtype,bias_dtype", [([4096, 512], 9216, 3072, torch.bfloat16, torch.bfloat16),
+                                                     ([1024, 4096, 512], 4096, 512, torch.float16, None),
+                                                     ([512, 2048], 32768, 768, torch.bfloat16, torch.float32)])
+def test_multi_round_grouped_gemm_bit_exact(gpu, ms, n, k, dtype, bias_dtype):
+    """Grouped launches of more than one round (FLUX's img + txt qkv is 648
+    tiles): every problem equals its int32 product + rescale bit for bit;
+    the first rows of the first problem equal the oracle."""
+    items = []
+    for i, m in enumerate(ms):
+        q, w, sx, sw = _qw(m, n, k, 30 + i)
+        b = (torch.randn(n, generator=torch.Generator().manual_seed(35 + i)) * 0.5).to(bias_dtype) \
+            if bias_dtype is not None else None
+        items.append((q, w, sx, sw, b))
+    q, w, sx, sw, b = items[0]
+    ref = OG.rescale(OG.int_mm(q[:64].numpy(), w.numpy()), sx[:64].numpy(), sw.numpy(),
+                     np32(b) if b is not None else None, DT[dtype])
+    items = [tuple(t.to(gpu) if t is not None else None for t in it) for it in items]
+    outs = _int8._gemm_grouped(items, dtype)
+    assert np.array_equal(np32(outs[0][:64]).view(np.uint32), ref.view(np.uint32))
+    for (q, w, sx, sw, b), out in zip(items, outs):
+        assert torch.equal(out, _int32_then_rescale(q, w, sx, sw, b, dtype))
+    assert all(torch.equal(a, c) for a, c in zip(_int8._gemm_grouped(items, dtype), outs))
