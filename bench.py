@@ -32,6 +32,7 @@ The same run also measures, and adds to the JSON line:
 
     python bench.py [--steps K] [--warmup W] [--no-full] [--no-cpu]
     python bench.py --copy-calibration   # 1 GiB device copy for counter scaling
+    python bench.py --cpu-configs        # the reference's CPU path at every config shape (host cores only)
     python bench.py --mfma-ceiling       # MFMA-only throughput (int8, bf16)
     python bench.py --shapes             # per-shape report for every BASELINE config (+ the GEMM A/B)
     python bench.py --gemm-ab            # same-process GEMM A/B against torch._int_mm (hipBLASLt)
@@ -372,6 +373,59 @@ def cpu_cfg1(budget_s: float = 4.0):
                     "quantize_rows -> torch._int_mm -> rescale on the CPU",
             "ms_per_call": round(ms, 3), "TOPS": round(2 * 8192 * 1280 * 320 / (ms * 1e-3) / 1e12, 4),
             "cores": torch.get_num_threads(), "calls": n}
+
+
+def cpu_configs(budget_s: float = 2.0) -> None:
+    """The reference's CPU path (oracle/cpu_path.py: the W8A8 linear as
+    quantize_rows(rotate(x)) -> torch._int_mm -> rescale; attention as fp32
+    SDPA, where the int8 backend falls through on CPU) at each BASELINE config
+    shape, on all host threads. Each shape runs on a sample of its rows or
+    queries (all keys, all heads) for about ``budget_s`` and is scaled to the
+    full call by its share of the work; one JSON line per shape."""
+    from oracle import cpu_path as C
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+
+    def timed(fn):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                return el / n
+
+    def attn(name, B, H, Sq, Skv, D, rows):
+        rows = min(rows, Sq)
+        q = torch.randn(B, H, rows, D, generator=g)
+        k = torch.randn(B, H, Skv, D, generator=g)
+        v = torch.randn(B, H, Skv, D, generator=g)
+        t = timed(lambda: C.attention_bhld(q, k, v)) * Sq / rows
+        print(json.dumps({"kind": "cpu_attention", "shape": name, "B": B, "H": H, "Sq": Sq, "Skv": Skv, "D": D,
+                          "sample_queries": rows, "ms_per_call": round(t * 1e3, 3),
+                          "TOPS": round(4 * B * H * Sq * Skv * D / t / 1e12, 4), "cores": torch.get_num_threads()}),
+              flush=True)
+
+    def lin(name, M, K, N, group, dtype, rows):
+        rows = min(rows, M)
+        w = torch.randn(N, K, generator=g) * 0.02
+        w8, sw = C.quantize_rows(C.rotate(w, group) if group else w)
+        x = torch.randn(rows, K, generator=g).to(dtype)
+        b = (torch.randn(N, generator=g) * 0.02).to(dtype)
+        t = timed(lambda: C.w8a8_linear(x, w8, sw, b, group)) * M / rows
+        print(json.dumps({"kind": "cpu_w8a8_linear", "shape": name, "M": M, "K": K, "N": N, "group": group,
+                          "sample_rows": rows, "ms_per_call": round(t * 1e3, 3),
+                          "TOPS": round(2 * M * N * K / t / 1e12, 4), "cores": torch.get_num_threads()}),
+              flush=True)
+
+    cfg1 = cpu_cfg1(budget_s)
+    print(json.dumps({"kind": "cpu_w8a8_linear", "shape": "cfg1_sd15_ff", "M": 8192, "K": 320, "N": 1280, "group": 0,
+                      "sample_rows": 8192, **{k: cfg1[k] for k in ("ms_per_call", "TOPS", "cores")}}), flush=True)
+    for name, B, H, Sq, Skv, D, _dt, _off in ATTN_SHAPES:
+        attn(name, B, H, Sq, Skv, D, 256 if Skv > 1000 else Sq)
+    for name, M, K, N, dt in LIN_SHAPES:
+        lin(name, M, K, N, 256 if K % 256 == 0 else 0, dt, 256)
 
 
 # ---------------------------------------------------------------- per-shape report
@@ -730,12 +784,18 @@ def main():
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only measure the MFMA-only throughput of the device (int8 and bf16, 1 and 2 waves per "
                          "SIMD, constant and changing operands) and exit")
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="only time the reference's CPU path at every BASELINE config shape (bounded row / query "
+                         "samples scaled to a full call, all host threads) and exit (no GPU)")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only summarize rocprofv3 FETCH_SIZE / WRITE_SIZE runs under DIR (copy_* and step_*) "
                          "into profiles/gemm_flux_step_traffic.json and exit (no GPU)")
     args = ap.parse_args()
     if args.traffic_from:
         traffic_summary(Path(args.traffic_from))
+        return
+    if args.cpu_configs:
+        cpu_configs()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one MI355X); "
