@@ -174,7 +174,8 @@ enum {
   DC_GEMM_PLAN_256x256 = 0,      /* 8 waves, 128 x 64 wave tiles, register-staged loads */
   DC_GEMM_PLAN_192x256 = 1,      /* 8 waves, 96 x 64 wave tiles */
   DC_GEMM_PLAN_128x128 = 2,      /* 4 waves, 64 x 64 wave tiles, 2 workgroups per CU */
-  DC_GEMM_PLAN_DMA_256x256 = 3   /* 4 waves, 128 x 128 wave tiles, loads straight into LDS */
+  DC_GEMM_PLAN_DMA_256x256 = 3,  /* 4 waves, 128 x 128 wave tiles, loads straight into LDS */
+  DC_GEMM_PLAN_192x128 = 4       /* 192 (n) x 128 (m) on 4 waves, 96 x 64 wave tiles, 1 workgroup per CU */
 };
 int dc_w8a8_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw);
 

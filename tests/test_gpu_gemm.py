@@ -146,7 +146,8 @@ def test_short_input(gpu):
 # K tails among them
 TILE_SHAPES = [((4096, 12288, 512), "dma_256x256"), ((4608, 3072, 256), "dma_256x256"),
                ((4096, 12288, 272), "256x256"), ((4096, 3072, 512), "192x256"),
-               ((4000, 3000, 272), "192x256"), ((512, 3072, 512), "128x128"), ((4001, 12200, 768), "dma_256x256")]
+               ((4000, 3000, 272), "192x256"), ((512, 3072, 512), "128x128"), ((4001, 12200, 768), "dma_256x256"),
+               ((512, 12288, 3072), "192x128"), ((500, 12200, 336), "192x128")]
 
 
 @pytest.mark.parametrize("mnk,plan", TILE_SHAPES)
