@@ -488,6 +488,7 @@ __global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
   constexpr int CPR = BK / 16;                    // 16-byte chunks per row
   constexpr int NWL = BN * CPR / NT, NAL = BM * CPR / NT;
   static_assert(BN * CPR % NT == 0 && BM * CPR % NT == 0, "tile must split evenly over the threads");
+  static_assert(BN <= NT && BM <= NT, "EpiRegs holds one epilogue-vector entry per thread");
   constexpr int STAGE = (BN + BM) * PITCH;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
