@@ -367,6 +367,26 @@ def test_argument_checks_fail_before_any_launch():
     assert so.dc_w8a8_gemm_group_plan(Ms, 0, 3072, 3072) == -1
 
 
+def test_bench_cpu_configs_reports_every_shape(monkeypatch, capsys):
+    """`bench.py --cpu-configs` (the reference's CPU path per config shape,
+    sampled and scaled to a whole call) on two small shapes: one JSON line
+    per shape plus config 1, each with a positive time, its sample and the
+    thread count."""
+    import json
+    sys.path.insert(0, str(ROOT))
+    import bench
+    monkeypatch.setattr(bench, "ATTN_SHAPES", [("tiny_self", 1, 2, 300, 300, 40, torch.float16, 0.0)])
+    monkeypatch.setattr(bench, "LIN_SHAPES", [("tiny_linear", 300, 512, 384, torch.bfloat16)])
+    monkeypatch.setattr(bench, "cpu_cfg1", lambda budget_s: {"ms_per_call": 1.0, "TOPS": 1.0, "cores": 1})
+    bench.cpu_configs(budget_s=0.01)
+    rows = [json.loads(l) for l in capsys.readouterr().out.splitlines() if l.startswith("{")]
+    assert [r["shape"] for r in rows] == ["cfg1_sd15_ff", "tiny_self", "tiny_linear"]
+    att, lin = rows[1], rows[2]
+    assert att["kind"] == "cpu_attention" and att["sample_queries"] == 300 and att["ms_per_call"] > 0
+    assert lin["kind"] == "cpu_w8a8_linear" and lin["sample_rows"] == 256 and lin["group"] == 256
+    assert lin["ms_per_call"] > 0 and lin["cores"] == torch.get_num_threads()
+
+
 def test_bench_refuses_more_than_one_gpu():
     res = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                          timeout=120)
