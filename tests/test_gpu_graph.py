@@ -6,9 +6,9 @@ synchronizations, the outputs are overwritten with NaN before each replay
 captured input buffers must reach the next replay.
 
 Covered: the quantize kernel, each GEMM plan the FLUX step uses (DMA-fed
-256 x 256, 192 x 256 / 128 x 128, split-K with its workspace and epilogue
-pass, a grouped launch of two layers, the same pair with the gated
-residual epilogue) and the INT8 attention (K statistics, K quantize, attention): the
+256 x 256, 192 x 128 at the text MLP-up shape, 192 x 256 / 128 x 128,
+split-K with its workspace and epilogue pass, a grouped launch of two
+layers, the same pair with the gated residual epilogue) and the INT8 attention (K statistics, K quantize, attention): the
 256-query kernel at the FLUX shape, stream-K pieces and their merge at SDXL's
 4096-token self-attention, and the 128-query kernel whole.
 """
@@ -24,9 +24,12 @@ from diffucore_amd import _int8, attention_bhld
 pytestmark = pytest.mark.gpu
 
 BF16 = torch.bfloat16
-# (M, K, N): DMA-fed 256 x 256 plan, split-K (M = 512, K = 3072), a ragged one;
-# the last two run as one grouped launch (dc_w8a8_gemm_grouped)
-LINEARS = [(4096, 512, 4096), (512, 3072, 3072), (1000, 768, 1280), (1024, 512, 1024), (300, 512, 1024)]
+# (M, K, N): DMA-fed 256 x 256 plan, split-K (M = 512, K = 3072), 192 x 128
+# tiles (FLUX's text MLP up), a ragged one; the last two run as one grouped
+# launch (dc_w8a8_gemm_grouped)
+LINEARS = [(4096, 512, 4096), (512, 3072, 3072), (512, 3072, 12288), (1000, 768, 1280), (1024, 512, 1024),
+           (300, 512, 1024)]
+NS = len(LINEARS) - 2   # the layers called one by one
 ATTN = [(1, 24, 4608, 128), (2, 10, 4096, 64), (1, 4, 1000, 64)]
 
 
@@ -36,19 +39,19 @@ def _case(gpu, seed):
     layers = [_int8.Int8Linear.from_linear(nn.Linear(k, n, bias=True).to(gpu).to(BF16), 256) for _, k, n in LINEARS]
     xs = [torch.randn(m, k, generator=g, device=gpu).to(BF16) for m, k, _ in LINEARS]
     # residuals and one-row gates for the gated pair (the last two layers)
-    xs += [torch.randn(m, n, generator=g, device=gpu).to(BF16) for m, _, n in LINEARS[3:]]
-    xs += [torch.randn(n, generator=g, device=gpu).to(BF16) for _, _, n in LINEARS[3:]]
+    xs += [torch.randn(m, n, generator=g, device=gpu).to(BF16) for m, _, n in LINEARS[NS:]]
+    xs += [torch.randn(n, generator=g, device=gpu).to(BF16) for _, _, n in LINEARS[NS:]]
     qkvs = [[torch.randn(b, h, l, d, generator=g, device=gpu).to(BF16) for _ in range(3)] for b, h, l, d in ATTN]
     return layers, xs, qkvs
 
 
 def _step(layers, xs, qkvs):
     ys = [layer.matmul_quantized(*_int8.quantize_activation(x, layer.group), BF16)
-          for layer, x in zip(layers[:3], xs[:3])]
-    ys += _int8.linear_group(layers[3:], xs[3:5])
-    qs = [_int8.quantize_activation(x, layer.group) for layer, x in zip(layers[3:], xs[3:5])]
-    ys += _int8.matmul_quantized_gated([(layer, *q, r, gt) for layer, q, r, gt in zip(layers[3:], qs, xs[5:7], xs[7:9])],
-                                       BF16)
+          for layer, x in zip(layers[:NS], xs[:NS])]
+    ys += _int8.linear_group(layers[NS:], xs[NS:NS + 2])
+    qs = [_int8.quantize_activation(x, layer.group) for layer, x in zip(layers[NS:], xs[NS:NS + 2])]
+    ys += _int8.matmul_quantized_gated([(layer, *q, r, gt) for layer, q, r, gt
+                                        in zip(layers[NS:], qs, xs[NS + 2:NS + 4], xs[NS + 4:NS + 6])], BF16)
     return ys + [attention_bhld(q, k, v, "int8_turing") for q, k, v in qkvs]
 
 
@@ -56,8 +59,10 @@ def test_graph_replays_equal_eager_calls(gpu):
     layers, xs, qkvs = _case(gpu, 3)
     m, k, n = LINEARS[0]
     assert _int8.gemm_plan(m, n, k) == "dma_256x256"
-    assert _int8.gemm_group_plan([LINEARS[3][0], LINEARS[4][0]], LINEARS[3][2], LINEARS[3][1])
-    assert all(x.data_ptr() % 16 == 0 for x in xs[5:])   # the gated pair takes the fused epilogue
+    if torch.cuda.get_device_properties(gpu).multi_processor_count == 256:
+        assert _int8.gemm_plan(LINEARS[2][0], LINEARS[2][2], LINEARS[2][1]) == "192x128"
+    assert _int8.gemm_group_plan([LINEARS[NS][0], LINEARS[NS + 1][0]], LINEARS[NS][2], LINEARS[NS][1])
+    assert all(x.data_ptr() % 16 == 0 for x in xs[NS + 2:])   # the gated pair takes the fused epilogue
     with torch.no_grad():
         want = [t.clone() for t in _step(layers, xs, qkvs)]
         side = torch.cuda.Stream()
