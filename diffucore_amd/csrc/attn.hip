@@ -12,11 +12,16 @@
 //  2. kquant_kernel  ksum = sequential sum over windows (:137-142); K smoothed by
 //                    its mean, val = fma(-ksum, 1/L, k), quantized per 64-key
 //                    block (:38-90) into the workspace.
-//  3. attn_kernel    Q quantized per token in-kernel (:341-388); S^T = K Q^T on
+//  3. attn_wide_kernel or attn_kernel (+ attn_merge_kernel for stream-K plans)
+//                    Q quantized per token in-kernel (:341-388); S^T = K Q^T on
 //                    v_mfma_i32_32x32x32_i8 (int32, exact); base-2 online softmax
 //                    in float32 on the logits S * (qs*sm_scale*log2e * ks_block);
 //                    P rounded to the 16-bit input type; O^T = V^T P^T on
 //                    v_mfma_f32_32x32x16_{bf16,f16} with float32 accumulation.
+//                    attn_wide_kernel (K / V DMA-fed into an LDS ring) runs
+//                    whole query tiles: 256 rows at Dp = 128 when they fill a
+//                    workgroup per CU, 128 rows at Dp = 64 when the plan has no
+//                    stream-K split; attn_kernel runs the rest.
 //
 // attn_kernel: a workgroup owns 128 query rows of one (batch, head), 4 waves x
 // 32 rows. Computing S^T and O^T (instead of S and O) makes every accumulator
@@ -55,7 +60,7 @@ struct AttnArgs {
   // tiles 0 .. dp_blocks - 1 whole; the sk_blocks blocks after them share the
   // (query tile, key tile) pairs of the last sk_tiles query tiles
   int dp_blocks, sk_blocks, sk_tiles;
-  int wide;   // 1: attn_wide_kernel runs the dp_blocks 256-query tiles
+  int wide;   // 1: attn_wide_kernel runs the dp_blocks query tiles (Wide<Dp>::BQW rows each)
   int64_t qsb, qsl, qsh, ksb, ksl, ksh, vsb, vsl, vsh, osb, osl, osh;
   float scale_log2;
 };
@@ -814,21 +819,27 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs p) {
 }
 
 
-// ---------------------------------------------------------------- 3b. attention for D > 64: DMA-fed, 256 queries per workgroup
+// ---------------------------------------------------------------- 3b. DMA-fed attention (attn_wide_kernel)
 //
-// attn_wide_kernel: head dims 65 .. 128 (Dp = 128), key ranges up to
-// WIDE_MAX_TILES tiles. A workgroup owns 256 query rows of one (b, h): 8 waves
-// of 32 rows, two per SIMD, all fed by one stream of K / V tiles. K (int8,
-// from the workspace) and V (16-bit, read in place) go from global memory
-// straight into LDS (global_load_lds: no staging registers, no LDS store
-// instructions) through a ring of ATTN_WIDE_STAGES stages of one 64-key tile
-// each, loaded 3 tiles ahead. Instead of padded rows, XOR swizzles keep the
-// operand reads conflict-free (0 bank conflicts counted):
-//   K row r (128 B): 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7), so the
-//     16 rows one ds_read_b128 serves per cycle cover all banks;
-//   V row r (256 B): 64-byte segment g stored at segment g ^ (r & 3), so the
-//     4 rows a 16-lane ds_read_b64_tr_b16 group reads lie in 4 different
-//     segments.
+// attn_wide_kernel<DT, DP>: key ranges up to WIDE_MAX_TILES tiles.
+//   Dp = 128 (head dims 65 .. 128): a workgroup owns 256 query rows of one
+//     (b, h), 8 waves of 32 rows, two per SIMD, one workgroup per CU.
+//   Dp = 64 (head dims <= 64): 128 query rows, 4 waves, two workgroups per CU.
+// Either way the waves of a workgroup are fed by one stream of K / V tiles.
+// K (int8, from the workspace) and V (16-bit, read in place) go from global
+// memory straight into LDS (global_load_lds: no staging registers, no LDS
+// store instructions) through a ring of ATTN_WIDE_STAGES stages of one 64-key
+// tile each, loaded 3 tiles ahead: per tile and wave one DMA instruction of
+// K and two of V (a 64-key tile is Dp K bytes and 2 Dp V bytes per key, and
+// there are Dp / 16 waves of 64 lanes x 16 bytes). Instead of padded rows,
+// XOR swizzles keep the operand reads conflict-free (0 bank conflicts
+// counted at Dp = 128):
+//   K row r (Dp bytes, Dp / 16 chunks of 16 B): chunk c stored at chunk
+//     c ^ ((r / (256 / Dp)) % (Dp / 16)), so the rows one ds_read_b128 serves
+//     per cycle cover all banks;
+//   V row r (2 Dp bytes, Dp / 32 segments of 64 B): segment g stored at
+//     segment g ^ ((r / (128 / Dp)) % (Dp / 32)), so the 4 rows a 16-lane
+//     ds_read_b64_tr_b16 group reads lie in 4 different 64-byte bank ranges.
 // The K block scales are staged in LDS once, so no global load sits in the
 // loop (a uniform load there would be ordered behind the tile loads and wait
 // for them). Same arithmetic as attn_kernel; the iteration is described at
@@ -840,12 +851,27 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs p) {
 // (34% busy) work barely overlap on a SIMD: a microbenchmark of one tile's
 // mix (24 MFMAs, ~100 softmax VALU instructions) runs at about the sum of
 // the two alone however it is arranged.
-constexpr int BQW = 256;                            // query rows per workgroup
+template <int DP>
+struct Wide {
+  static constexpr int NW = DP / 16;                  // waves per workgroup
+  static constexpr int NT = 64 * NW;                  // threads
+  static constexpr int BQW = 32 * NW;                 // query rows per workgroup
+  static constexpr int ND = DP / 32;                  // 32-channel blocks of d
+  static constexpr int WK = BKEY * DP;                // int8 K tile bytes
+  static constexpr int WV = BKEY * 2 * DP;            // 16-bit V tile bytes
+  static constexpr int WSTAGE = WK + WV;              // 24 KB / 12 KB
+  static constexpr int KC = DP / 16;                  // 16-byte chunks per K row
+  static constexpr int KSH = DP == 128 ? 1 : 2;       // log2(K rows per 256 bytes)
+  static constexpr int VR = 2 * DP;                   // V row bytes
+  static constexpr int VS = DP / 32;                  // 64-byte segments per V row
+  static constexpr int VSH = DP == 128 ? 0 : 1;       // log2(V rows per 256 bytes)
+  static constexpr int KRW = 1024 / DP;               // K rows per wave DMA
+  static constexpr int VRW = 512 / DP;                // V rows per wave DMA
+  static constexpr int BLOCKS = DP == 128 ? 1 : 2;    // workgroups per CU
+  static_assert(DP == 64 || DP == 128, "Dp is 64 or 128");
+  static_assert(NW * KRW == BKEY && 2 * NW * VRW == BKEY, "one K and two V DMAs per wave cover a tile");
+};
 constexpr int ATTN_WIDE_STAGES = 4;
-constexpr int WK_BYTES = BKEY * 128;                // int8 K tile
-constexpr int WV_BYTES = BKEY * 256;                // 16-bit V tile
-constexpr int WSTAGE = WK_BYTES + WV_BYTES;         // 24 KB
-constexpr int ATTN_WIDE_LDS = ATTN_WIDE_STAGES * WSTAGE;
 constexpr int WIDE_LOADS = 3;                       // DMA instructions per wave per tile: 1 K + 2 V
 constexpr int WIDE_MAX_TILES = 2048;                // K block scales staged in LDS: Lk <= 131072
 // V row strides (elements) below which a tile's 64 V rows span under 2^31
@@ -878,33 +904,39 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_ptr_t)(const_cast<void*>(p)));
 }
 
-// The 8 K operands (k-step ks, key block kb) of one 64-key tile from a
+// The 2 Dp / 32 K operands (k-step ks, key block kb) of one 64-key tile from a
 // swizzled K stage; kfo[ks] is the lane's byte offset of its 16-byte chunk for
 // k-step ks (row l32).
-__device__ __forceinline__ void k_operands(const uint8_t* __restrict__ sK, const int (&kfo)[4], v4i (&ka)[8]) {
+template <int DP>
+__device__ __forceinline__ void k_operands(const uint8_t* __restrict__ sK, const int (&kfo)[DP / 32],
+                                           v4i (&ka)[DP / 16]) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < DP / 32; ++ks)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) ka[2 * ks + kb] = *reinterpret_cast<const v4i*>(sK + kfo[ks] + (32 * kb) * 128);
+    for (int kb = 0; kb < 2; ++kb) ka[2 * ks + kb] = *reinterpret_cast<const v4i*>(sK + kfo[ks] + (32 * kb) * DP);
 }
 
 // S^T + magic from the K operands (`magic` holds MAGIC_I in every register: the
 // first k-step accumulates onto it, so the scores need no initialization).
-__device__ __forceinline__ void qk_mfma(const v4i (&ka)[8], const v4i (&qf)[4], const v16i& magic, v16i (&s)[2]) {
+template <int DP>
+__device__ __forceinline__ void qk_mfma(const v4i (&ka)[DP / 16], const v4i (&qf)[DP / 32], const v16i& magic,
+                                        v16i (&s)[2]) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < DP / 32; ++ks)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
       s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[2 * ks + kb], qf[ks], ks == 0 ? magic : s[kb], 0, 0, 0);
 }
 
-// V^T operand f (16-key step kk = f / 4, channel block i = f % 4) from a
+// V^T operand f (16-key step kk = f / ND, channel block i = f % ND) from a
 // swizzled V stage by two ds_read_tr16_b64; vfo[i] is the lane's byte offset
 // for channel block i (keys 4 hf + li / 4, + 8 for the second read).
-__device__ __forceinline__ v4i v_operand(const uint8_t* __restrict__ sV, const int (&vfo)[4], int f) {
-  const uint8_t* a = sV + vfo[f & 3] + (16 * (f >> 2)) * 256;
+template <int DP>
+__device__ __forceinline__ v4i v_operand(const uint8_t* __restrict__ sV, const int (&vfo)[DP / 32], int f) {
+  constexpr int ND = DP / 32, VR = 2 * DP;
+  const uint8_t* a = sV + vfo[f % ND] + (16 * (f / ND)) * VR;
   const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(const_cast<uint8_t*>(a)));
-  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(const_cast<uint8_t*>(a + 8 * 256)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(const_cast<uint8_t*>(a + 8 * VR)));
   return v4i{(int)((uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16)),
              (int)((uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16)),
              (int)((uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16)),
@@ -915,33 +947,35 @@ __device__ __forceinline__ v4i v_operand(const uint8_t* __restrict__ sV, const i
 constexpr int VPRE = 4;
 
 
-template <int DT>
-__global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[ATTN_WIDE_LDS];
+template <int DT, int DP>
+__global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kernel(AttnArgs p) {
+  using W = Wide<DP>;
+  constexpr int ND = W::ND;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[ATTN_WIDE_STAGES * W::WSTAGE];
   __shared__ float ks_l[WIDE_MAX_TILES];   // the (b, h)'s K block scales
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hf = lane >> 5, l32 = lane & 31;
-  const int nqt = (p.Lq + BQW - 1) / BQW;
+  const int nqt = (p.Lq + W::BQW - 1) / W::BQW;
   const int qlog = xcd_order(blockIdx.x, gridDim.x);
   const int qt = qlog % nqt, bh = qlog / nqt, b = bh / p.H, h = bh % p.H;
   const int ntiles = p.Lk64 / BKEY;
   const bool ragged = p.Lk % BKEY != 0;
 
   // ---- DMA sources (byte offsets from the tile's first row). K: wave w
-  // loads rows 8 w + lane / 8, physical chunk lane % 8, logical chunk
-  // (lane % 8) ^ ((row >> 1) & 7). V: rows 4 (w + 8 u) + lane / 16 (u = 0, 1),
-  // physical chunk lane % 16, logical chunk (lane % 16) ^ ((row & 3) << 2),
-  // clamped to the last chunk inside D (channels past D feed O rows that are
-  // never stored).
-  const int8_t* kg = p.k8 + (int64_t)bh * p.Lk64 * 128;
+  // loads rows KRW w + lane / KC, physical chunk lane % KC, logical chunk
+  // (lane % KC) ^ ((row >> KSH) % KC). V: rows VRW (w + NW u) + lane / (2 KC)
+  // (u = 0, 1), physical chunk lane % (2 KC) in segment (lane % (2 KC)) / 4,
+  // logical segment physical ^ ((row >> VSH) % VS), the chunk clamped to the
+  // last one inside D (channels past D feed O rows that are never stored).
+  const int8_t* kg = p.k8 + (int64_t)bh * p.Lk64 * DP;
   const uint16_t* vg = static_cast<const uint16_t*>(p.v) + b * p.vsb + h * p.vsh;
-  const int krow = 8 * w + (lane >> 3);
-  const uint32_t koff = (uint32_t)(krow * 128 + 16 * ((lane & 7) ^ ((krow >> 1) & 7)));
+  const int krow = W::KRW * w + lane / W::KC;
+  const uint32_t koff = (uint32_t)(krow * DP + 16 * ((lane % W::KC) ^ ((krow >> W::KSH) % W::KC)));
   int vrow[2], vcol[2];
   uint32_t voff[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    vrow[u] = 4 * (w + 8 * u) + (lane >> 4);
-    vcol[u] = min((lane & 15) ^ ((vrow[u] & 3) << 2), p.D / 8 - 1) * 8;
+    vrow[u] = W::VRW * (w + W::NW * u) + lane / (2 * W::KC);
+    vcol[u] = min((lane % (2 * W::KC)) ^ (((vrow[u] >> W::VSH) % W::VS) << 2), p.D / 8 - 1) * 8;
     voff[u] = (uint32_t)(vrow[u] * (int)p.vsl + vcol[u]) * 2u;   // the host keeps p.vsl < WIDE_MAX_VSL
   }
   // tile `tile` into stage `st` (tile % STAGES); past the end the source is
@@ -949,20 +983,20 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
   // the wave's DMA destinations in stage 0 (K, then V rows of u = 0, 1)
   const uint32_t lds0 = lds_addr(lds) + 1024 * w;
   auto issue = [&](int tile, int st) __attribute__((always_inline)) {
-    const uint32_t sb = lds0 + st * WSTAGE;
+    const uint32_t sb = lds0 + st * W::WSTAGE;
     tile = min(tile, ntiles - 1);
-    dma16(reinterpret_cast<const uint8_t*>(kg) + tile * (BKEY * 128), koff, sb);
+    dma16(reinterpret_cast<const uint8_t*>(kg) + tile * (BKEY * DP), koff, sb);
     const uint16_t* vt = vg + (int64_t)tile * BKEY * p.vsl;
     if (ragged && tile == ntiles - 1) {
       // keys past Lk read key Lk - 1 (their probabilities are 0; the values stay finite)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int key = min(tile * BKEY + vrow[u], p.Lk - 1) - tile * BKEY;
-        dma16(vt, (uint32_t)(key * (int)p.vsl + vcol[u]) * 2u, sb + WK_BYTES + 8192 * u);
+        dma16(vt, (uint32_t)(key * (int)p.vsl + vcol[u]) * 2u, sb + W::WK + 1024 * W::NW * u);
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) dma16(vt, voff[u], sb + WK_BYTES + 8192 * u);
+      for (int u = 0; u < 2; ++u) dma16(vt, voff[u], sb + W::WK + 1024 * W::NW * u);
     }
   };
 
@@ -971,37 +1005,39 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
   issue(2, 2);
   // block scales into LDS (ordinary loads, waited for here, before any DMA
   // wait counts rely on the load order)
-  for (int i = t; i < ntiles; i += 512) ks_l[i] = p.ks[(int64_t)bh * ntiles + i];
+  for (int i = t; i < ntiles; i += W::NT) ks_l[i] = p.ks[(int64_t)bh * ntiles + i];
 
   // ---- Q: the wave's 32 rows, quantized per token into MFMA B operands
-  v4i qf[4];
+  v4i qf[ND];
   float cq;
-  const int qrow = qt * BQW + w * 32 + l32;
+  const int qrow = qt * W::BQW + w * 32 + l32;
   {
     const bool valid = qrow < p.Lq;
     const uint16_t* src = static_cast<const uint16_t*>(p.q) + b * p.qsb + (int64_t)(valid ? qrow : 0) * p.qsl + h * p.qsh;
-    cq = quantize_q_row<DT, 128>(src, valid, p.D, hf, qf) * p.scale_log2;
+    cq = quantize_q_row<DT, DP>(src, valid, p.D, hf, qf) * p.scale_log2;
   }
 
   // ---- operand offsets. K (A of S^T = K Q^T): row 32 kb + l32, logical chunk
-  // 2 ks + hf, physical (2 ks + hf) ^ ((l32 >> 1) & 7) = 2 ks ^ (hf ^ ((l32 >> 1) & 7)).
-  const int kx = hf ^ ((l32 >> 1) & 7);
-  int kfo[4];
+  // 2 ks + hf, physical (2 ks + hf) ^ ((l32 >> KSH) % KC) (32 kb leaves the
+  // swizzle unchanged).
+  const int kx = (l32 >> W::KSH) % W::KC;
+  int kfo[ND];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) kfo[ks] = l32 * 128 + 16 * ((2 * ks) ^ kx);
+  for (int ks = 0; ks < ND; ++ks) kfo[ks] = l32 * DP + 16 * ((2 * ks + hf) ^ kx);
   // V^T (A of O^T = V^T P^T) by ds_read_tr16_b64: 16-lane group g16 of half hf
   // reads keys 16 kk + 4 hf + li / 4 (+ 8), channels 32 i + 16 g16 + 4 (li % 4);
-  // such a key's row has (row & 3) = li / 4, so channel block i sits at
-  // segment i ^ (li / 4)
+  // such a key's row r has (r >> VSH) % VS = ((li / 4) >> VSH) % VS, so channel
+  // block i sits at segment i ^ that
   const int li = lane & 15, g16 = (lane >> 4) & 1;
-  int vfo[4];
+  const int vx = ((li >> 2) >> W::VSH) % W::VS;
+  int vfo[ND];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) vfo[i] = (4 * hf + (li >> 2)) * 256 + 64 * (i ^ (li >> 2)) + 32 * g16 + 8 * (li & 3);
+  for (int i = 0; i < ND; ++i) vfo[i] = (4 * hf + (li >> 2)) * W::VR + 64 * (i ^ vx) + 32 * g16 + 8 * (li & 3);
 
   float m = -INFINITY, lsum = 0.f;
-  v16f o[4];
+  v16f o[ND];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = v16f{0.f};
+  for (int i = 0; i < ND; ++i) o[i] = v16f{0.f};
   v16i magic;
 #pragma unroll
   for (int j = 0; j < 16; ++j) magic[j] = MAGIC_I;
@@ -1024,40 +1060,40 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     issue(tile + 3, (st + 3) % ATTN_WIDE_STAGES);
-    const uint8_t* sv = lds + st * WSTAGE + WK_BYTES;
-    v4i ka[8], va[16];
-    k_operands(lds + ((st + 1) % ATTN_WIDE_STAGES) * WSTAGE, kfo, ka);
+    const uint8_t* sv = lds + st * W::WSTAGE + W::WK;
+    v4i ka[2 * ND], va[4 * ND];
+    k_operands<DP>(lds + ((st + 1) % ATTN_WIDE_STAGES) * W::WSTAGE, kfo, ka);
 #pragma unroll
-    for (int f = 0; f < VPRE; ++f) va[f] = v_operand(sv, vfo, f);
+    for (int f = 0; f < VPRE; ++f) va[f] = v_operand<DP>(sv, vfo, f);
     __builtin_amdgcn_sched_barrier(0);
     const int key0 = tile * BKEY + 4 * hf;
     const float c = cq * ks_l[tile];
     uint32_t pk[2][8];
     float ts = 0.f;
-    qk_mfma(ka, qf, magic, nxt);
+    qk_mfma<DP>(ka, qf, magic, nxt);
     softmax_exp<DT, TAIL>(cur, key0, p.Lk, c, __builtin_fmaf(MAGIC_F, c, m), ts, pk);
     // 56 of the ~96 VALU instructions of the exponentials first (the K
     // operand reads issued after the barrier land meanwhile, so the first
-    // QK^T MFMA of tile + 1 does not hold up the in-order issue), then the 8
-    // MFMAs with 5 VALU instructions behind each. Measured at FLUX against
+    // QK^T MFMA of tile + 1 does not hold up the in-order issue), then the
+    // 2 ND MFMAs with the rest spread behind them. Measured at FLUX against
     // one MFMA then 12 VALU from the start: 2.7% faster per call, same bits;
     // 48 to 72 up front measure alike, all of it up front is slower.
     __builtin_amdgcn_sched_group_barrier(0x002, 56, 0);
 #pragma unroll
-    for (int z = 0; z < 8; ++z) {
+    for (int z = 0; z < 2 * ND; ++z) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 40 / (2 * ND), 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    lazy_fixup<DT, 128, TAIL>(cur, key0, p.Lk, c, m, lsum, ts, o, pk);
+    lazy_fixup<DT, DP, TAIL>(cur, key0, p.Lk, c, m, lsum, ts, o, pk);
     __builtin_amdgcn_sched_barrier(0);
     // PV: MFMA f consumes V operand f, read VPRE MFMAs earlier
 #pragma unroll
-    for (int f = 0; f < 16; ++f) {
-      if (f + VPRE < 16) va[f + VPRE] = v_operand(sv, vfo, f + VPRE);
-      const int kk = f >> 2, kb = kk >> 1, j0 = 4 * (kk & 1);
+    for (int f = 0; f < 4 * ND; ++f) {
+      if (f + VPRE < 4 * ND) va[f + VPRE] = v_operand<DP>(sv, vfo, f + VPRE);
+      const int kk = f / ND, kb = kk >> 1, j0 = 4 * (kk & 1);
       const v4i pf = {(int)pk[kb][j0], (int)pk[kb][j0 + 1], (int)pk[kb][j0 + 2], (int)pk[kb][j0 + 3]};
-      o[f & 3] = mfma_pv<DT>(va[f], pf, o[f & 3]);
+      o[f % ND] = mfma_pv<DT>(va[f], pf, o[f % ND]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -1067,9 +1103,9 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
   DC_ATTN_WAIT_VMCNT(2 * WIDE_LOADS);
   __syncthreads();
   {
-    v4i ka[8];
-    k_operands(lds, kfo, ka);
-    qk_mfma(ka, qf, magic, sa);
+    v4i ka[2 * ND];
+    k_operands<DP>(lds, kfo, ka);
+    qk_mfma<DP>(ka, qf, magic, sa);
   }
   // the last tile of a ragged key range runs masked, after the others; the
   // loop takes 4 tiles per trip (stages 0 .. 3 as constants), then 0 to 3 more
@@ -1097,7 +1133,7 @@ __global__ void __launch_bounds__(512, 1) attn_wide_kernel(AttnArgs p) {
     const float inv = 1.f / lsum;
     uint16_t* dst = static_cast<uint16_t*>(p.o) + b * p.osb + (int64_t)qrow * p.osl + h * p.osh;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < ND; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * i + 8 * g + 4 * hf;
@@ -1182,18 +1218,27 @@ static int attn_cus() {
 
 template <int DP>
 static AttnPlan attn_plan_dp(int dtype, int B, int H, int Lq, int Lk) {
+  const bool wide_ok = (Lk + BKEY - 1) / BKEY <= WIDE_MAX_TILES;
   if constexpr (DP == 128) {
     // attn_wide_kernel (whole 256-row query tiles, no stream-K split) when its
     // tiles fill at least one workgroup per CU; smaller grids keep the
     // 128-row tiles, which spread the work over twice the workgroups
     // (measured at 1 x 4 x 1024 x 1024: 34.5 us against 40 us)
-    const int64_t wblocks = (int64_t)((Lq + BQW - 1) / BQW) * H * B;
-    if ((Lk + BKEY - 1) / BKEY <= WIDE_MAX_TILES && wblocks >= attn_cus()) return AttnPlan{(int)wblocks, 0, 0, true};
+    const int64_t wblocks = (int64_t)((Lq + Wide<128>::BQW - 1) / Wide<128>::BQW) * H * B;
+    if (wide_ok && wblocks >= attn_cus()) return AttnPlan{(int)wblocks, 0, 0, true};
   }
   const int64_t qtiles = (int64_t)((Lq + BQ - 1) / BQ) * H * B;
   const int ntiles = (Lk + BKEY - 1) / BKEY;
   const int slots = dtype == DC_BF16 ? attn_slots<DC_BF16, DP>() : attn_slots<DC_F16, DP>();
-  return attn_plan(qtiles, ntiles, slots);
+  AttnPlan pl = attn_plan(qtiles, ntiles, slots);
+  if constexpr (DP == 64) {
+    // at Dp = 64 attn_wide_kernel runs the same whole 128-row query tiles
+    // (two workgroups per CU, like attn_kernel); plans with a stream-K split
+    // keep attn_kernel
+    static_assert(Wide<64>::BQW == BQ, "the Dp = 64 wide tiles are attn_kernel's query tiles");
+    if (wide_ok && pl.sk_blocks == 0) pl.wide = true;
+  }
+  return pl;
 }
 
 struct WsLayout {
@@ -1226,11 +1271,9 @@ static int launch_attn(AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((kquant_kernel<DT, DP>), dim3((a.Lk64 / BKEY + KQ_BLOCKS - 1) / KQ_BLOCKS, a.H, a.B), dim3(256),
                      0, st, a);
   if (int e = launch_status("kquant_kernel")) return e;
-  if constexpr (DP == 128) {
-    if (a.wide) {
-      hipLaunchKernelGGL((attn_wide_kernel<DT>), dim3((unsigned)a.dp_blocks), dim3(512), 0, st, a);
-      return launch_status("attn_wide_kernel");
-    }
+  if (a.wide) {
+    hipLaunchKernelGGL((attn_wide_kernel<DT, DP>), dim3((unsigned)a.dp_blocks), dim3(Wide<DP>::NT), 0, st, a);
+    return launch_status("attn_wide_kernel");
   }
   hipLaunchKernelGGL((attn_kernel<DT, DP>), dim3((unsigned)(a.dp_blocks + a.sk_blocks)), dim3(256), 0, st, a);
   if (int e = launch_status("attn_kernel")) return e;

@@ -318,14 +318,42 @@ def test_growing_logits_rescale_128_query_kernel(gpu, B, H, L, D, dtype):
     assert r < ORACLE_REL[dtype] and c > ORACLE_COS
 
 
-def test_long_v_row_stride_takes_128_query_kernel(gpu):
-    """A V whose row stride puts a 64-key tile past 2^31 bytes (the 256-query
-    kernel's 32-bit DMA offsets) runs the 128-query kernel with whole tiles:
-    same inputs, V laid out with an L-stride of 2^23 elements, against the
-    same V contiguous, within the oracle bound of each other."""
-    B, Lq, Lk, H, D, dtype = 1, 512, 130, 256, 128, torch.bfloat16
-    if A.attn_plan(B, H, Lq, Lk, D, dtype)["dp_tiles"] != B * H * 2:
-        pytest.skip("this grid does not take the 256-query kernel on this device")
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 40])
+def test_growing_logits_rescale_dma_kernel_head_dim_64(gpu, D, dtype):
+    """The growing-logits case on the DMA-fed kernel at Dp = 64 (4 waves, 128
+    query rows per workgroup): a plan without stream-K pieces, row maxima
+    rising from ~8 to ~100 over the keys, so O is rescaled every few tiles.
+    Finite, and within the oracle bound."""
+    B, H, L = 1, 4, 1024
+    assert A.attn_plan(B, H, L, L, D, dtype) == {"dp_tiles": B * H * L // 128, "sk_blocks": 0, "sk_tiles": 0}
+    g = torch.Generator().manual_seed(5)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = (8 * u + 0.1 * torch.randn(B, L, H, D, generator=g)).to(dtype)
+    k = (100 * torch.linspace(0, 1, L).view(1, L, 1, 1) * u + torch.randn(B, L, H, D, generator=g)).to(dtype)
+    v = torch.randn(B, L, H, D, generator=g).to(dtype)
+    out, _ = _run(q, k, v, gpu)
+    assert torch.isfinite(out).all()
+    o = np32(out)
+    ora = OA.int8_attention(np32(q), np32(k), np32(v), D ** -0.5, DT[dtype], DT[dtype])
+    r, c = rel_l2(o, ora), cosine(o, ora)
+    print(f"[attn] growing logits Dp 64 DMA kernel D {D} {DT[dtype]}: vs oracle rel {r:.2e} cos {c:.7f}")
+    assert r < ORACLE_REL[dtype] and c > ORACLE_COS
+
+
+@pytest.mark.parametrize("H,D", [(256, 128), (64, 64)])
+def test_long_v_row_stride_takes_128_query_kernel(gpu, H, D):
+    """A V whose row stride puts a 64-key tile past 2^31 bytes (the DMA-fed
+    kernel's 32-bit offsets) runs the 128-query register-staged kernel with
+    whole tiles: same inputs, V laid out with an L-stride of 2^23 elements,
+    against the same V contiguous, within the oracle bound of each other. At
+    head dim 128 the grid is one that otherwise takes 256-query tiles; at 64
+    one that otherwise takes the 4-wave DMA-fed kernel."""
+    B, Lq, Lk, dtype = 1, 512, 130, torch.bfloat16
+    pl = A.attn_plan(B, H, Lq, Lk, D, dtype)
+    if pl["sk_blocks"] or (D == 128 and pl["dp_tiles"] != B * H * 2):
+        pytest.skip("this grid does not take the DMA-fed kernel on this device")
     q, k, v = _inputs(B, Lq, Lk, H, D, dtype, seed=8)
     qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
     vsl = 1 << 23
