@@ -19,9 +19,10 @@
 //                    P rounded to the 16-bit input type; O^T = V^T P^T on
 //                    v_mfma_f32_32x32x16_{bf16,f16} with float32 accumulation.
 //                    attn_wide_kernel (K / V DMA-fed into an LDS ring) runs
-//                    whole query tiles: 256 rows at Dp = 128 when they fill a
-//                    workgroup per CU, 128 rows at Dp = 64 when the plan has no
-//                    stream-K split; attn_kernel runs the rest.
+//                    whole 256-row query tiles at Dp = 128 when they fill a
+//                    workgroup per CU, and every Dp = 64 plan (128-row tiles,
+//                    stream-K pieces included); attn_kernel runs the rest
+//                    (smaller Dp = 128 grids, V row strides past 2^23).
 //
 // attn_kernel: a workgroup owns 128 query rows of one (batch, head), 4 waves x
 // 32 rows. Computing S^T and O^T (instead of S and O) makes every accumulator
@@ -947,18 +948,26 @@ __device__ __forceinline__ v4i v_operand(const uint8_t* __restrict__ sV, const i
 constexpr int VPRE = 4;
 
 
-template <int DT, int DP>
-__global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kernel(AttnArgs p) {
+// One piece of attn_wide_kernel's work: query tile `qlog` ((b, h, tile) in
+// that order) over key tiles tb .. te - 1, in the LDS ring `lds` with the K
+// block scales staged in `ks_l`. PIECE = false: the whole key range, the
+// output stored; otherwise the unnormalized O (P = 2^(logit - m)), the running
+// row maxima m and the row sums go to partial-result slot `slot`, in
+// attn_piece's layout (the tiles are BQ rows).
+template <int DT, int DP, bool PIECE>
+__device__ __forceinline__ void wide_piece(const AttnArgs& p, uint8_t* lds, float* ks_l, int qlog, int tb_, int te_,
+                                           int slot_) {
   using W = Wide<DP>;
   constexpr int ND = W::ND;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[ATTN_WIDE_STAGES * W::WSTAGE];
-  __shared__ float ks_l[WIDE_MAX_TILES];   // the (b, h)'s K block scales
+  static_assert(!PIECE || W::BQW == BQ, "partial results hold BQ-row tiles");
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hf = lane >> 5, l32 = lane & 31;
   const int nqt = (p.Lq + W::BQW - 1) / W::BQW;
-  const int qlog = xcd_order(blockIdx.x, gridDim.x);
   const int qt = qlog % nqt, bh = qlog / nqt, b = bh / p.H, h = bh % p.H;
   const int ntiles = p.Lk64 / BKEY;
-  const bool ragged = p.Lk % BKEY != 0;
+  // a whole query tile (PIECE = false) takes its key range as compile-time facts
+  const int tb = PIECE ? tb_ : 0, te = PIECE ? te_ : ntiles, slot = PIECE ? slot_ : -1;
+  // only the last key tile has keys past Lk
+  const bool ragged = te == ntiles && p.Lk % BKEY != 0;
 
   // ---- DMA sources (byte offsets from the tile's first row). K: wave w
   // loads rows KRW w + lane / KC, physical chunk lane % KC, logical chunk
@@ -978,13 +987,13 @@ __global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kern
     vcol[u] = min((lane % (2 * W::KC)) ^ (((vrow[u] >> W::VSH) % W::VS) << 2), p.D / 8 - 1) * 8;
     voff[u] = (uint32_t)(vrow[u] * (int)p.vsl + vcol[u]) * 2u;   // the host keeps p.vsl < WIDE_MAX_VSL
   }
-  // tile `tile` into stage `st` (tile % STAGES); past the end the source is
-  // the last tile again (in bounds; that data is never read)
+  // tile `tile` into stage `st` ((tile - tb) % STAGES); past the piece's end
+  // the source is its last tile again (in bounds; that data is never read)
   // the wave's DMA destinations in stage 0 (K, then V rows of u = 0, 1)
   const uint32_t lds0 = lds_addr(lds) + 1024 * w;
   auto issue = [&](int tile, int st) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + st * W::WSTAGE;
-    tile = min(tile, ntiles - 1);
+    tile = min(tile, te - 1);
     dma16(reinterpret_cast<const uint8_t*>(kg) + tile * (BKEY * DP), koff, sb);
     const uint16_t* vt = vg + (int64_t)tile * BKEY * p.vsl;
     if (ragged && tile == ntiles - 1) {
@@ -1000,12 +1009,12 @@ __global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kern
     }
   };
 
-  issue(0, 0);
-  issue(1, 1);
-  issue(2, 2);
-  // block scales into LDS (ordinary loads, waited for here, before any DMA
-  // wait counts rely on the load order)
-  for (int i = t; i < ntiles; i += W::NT) ks_l[i] = p.ks[(int64_t)bh * ntiles + i];
+  issue(tb, 0);
+  issue(tb + 1, 1);
+  issue(tb + 2, 2);
+  // the piece's block scales into LDS (ordinary loads, waited for here,
+  // before any DMA wait counts rely on the load order)
+  for (int i = tb + t; i < te; i += W::NT) ks_l[i] = p.ks[(int64_t)bh * ntiles + i];
 
   // ---- Q: the wave's 32 rows, quantized per token into MFMA B operands
   v4i qf[ND];
@@ -1042,7 +1051,7 @@ __global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kern
 #pragma unroll
   for (int j = 0; j < 16; ++j) magic[j] = MAGIC_I;
 
-  // Iteration `tile` (its stage st = tile % STAGES, passed as a constant in
+  // Iteration `tile` (its stage st = (tile - tb) % STAGES, passed as a constant in
   // the unrolled loop so every LDS address is a lane base plus an immediate).
   // One barrier: before it each wave waits for its own loads of tile + 1;
   // after it tile + 1 is complete in LDS for every wave, and every wave is
@@ -1099,7 +1108,7 @@ __global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kern
   };
 
   v16i sa[2], sb[2];
-  // tile 0 complete for every wave; the block scales are in LDS
+  // tile tb complete for every wave; the block scales are in LDS
   DC_ATTN_WAIT_VMCNT(2 * WIDE_LOADS);
   __syncthreads();
   {
@@ -1109,27 +1118,40 @@ __global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kern
   }
   // the last tile of a ragged key range runs masked, after the others; the
   // loop takes 4 tiles per trip (stages 0 .. 3 as constants), then 0 to 3 more
-  const int nfull = ragged ? ntiles - 1 : ntiles;
-  int tile = 0;
+  const int nfull = ragged ? te - 1 : te;
+  int tile = tb;
   for (; tile + 4 <= nfull; tile += 4) {
     step(tile, 0, sa, sb, std::false_type{});
     step(tile + 1, 1, sb, sa, std::false_type{});
     step(tile + 2, 2, sa, sb, std::false_type{});
     step(tile + 3, 3, sb, sa, std::false_type{});
   }
-  // remaining tiles: stage tile % 4 at run time, scores in sa
+  // remaining tiles: stage (tile - tb) % 4 at run time, scores in sa
   for (; tile < nfull; ++tile) {
-    step(tile, tile % ATTN_WIDE_STAGES, sa, sb, std::false_type{});
+    step(tile, (tile - tb) % ATTN_WIDE_STAGES, sa, sb, std::false_type{});
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) sa[kb] = sb[kb];
   }
-  if (ragged) step(tile, tile % ATTN_WIDE_STAGES, sa, sb, std::true_type{});
-  // no load may still be writing this workgroup's LDS when it ends
+  if (ragged) step(tile, (tile - tb) % ATTN_WIDE_STAGES, sa, sb, std::true_type{});
+  // no load may still be writing this workgroup's LDS when the piece ends
   DC_ATTN_WAIT_VMCNT(0);
 
   // ---- epilogue: O / l (each lane half summed its own keys)
   lsum += __shfl_xor(lsum, 32);
-  if (qrow < p.Lq) {
+  if constexpr (PIECE) {
+    float* part = p.part + (int64_t)slot * attn_part_floats<DP>();
+    const int r = w * 32 + l32;
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(part + r * DP + 32 * i + 8 * g + 4 * hf) =
+            make_float4(o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]);
+    if (hf == 0) {
+      part[BQ * DP + r] = m;
+      part[BQ * DP + BQ + r] = lsum;
+    }
+  } else if (qrow < p.Lq) {
     const float inv = 1.f / lsum;
     uint16_t* dst = static_cast<uint16_t*>(p.o) + b * p.osb + (int64_t)qrow * p.osl + h * p.osh;
 #pragma unroll
@@ -1142,6 +1164,35 @@ __global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kern
         const uint32_t hi = f32_to_h16<DT>(o[i][4 * g + 2] * inv) | (f32_to_h16<DT>(o[i][4 * g + 3] * inv) << 16);
         *reinterpret_cast<uint2*>(dst + d) = make_uint2(lo, hi);
       }
+  }
+}
+
+// Blocks 0 .. dp_blocks - 1 run whole query tiles (in XCD order). At Dp = 64
+// the sk_blocks blocks after them run the stream-K share of the last sk_tiles
+// query tiles as attn_kernel's do (pieces into partial slots 2 blk + piece,
+// combined by attn_merge_kernel).
+template <int DT, int DP>
+__global__ void __launch_bounds__(Wide<DP>::NT, Wide<DP>::BLOCKS) attn_wide_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[ATTN_WIDE_STAGES * Wide<DP>::WSTAGE];
+  __shared__ float ks_l[WIDE_MAX_TILES];   // the (b, h)'s K block scales
+  if ((int)blockIdx.x < p.dp_blocks) {
+    wide_piece<DT, DP, false>(p, lds, ks_l, xcd_order(blockIdx.x, p.dp_blocks), 0, 0, -1);
+    return;
+  }
+  if constexpr (DP == 64) {
+    const int ntiles = p.Lk64 / BKEY;
+    const int blk = xcd_order(blockIdx.x - p.dp_blocks, p.sk_blocks);
+    const int64_t units = (int64_t)p.sk_tiles * ntiles;
+    const int64_t u_end = sk_first(blk + 1, units, p.sk_blocks);
+    int64_t u = sk_first(blk, units, p.sk_blocks);
+    for (int piece = 0; u < u_end; ++piece) {
+      const int qi = (int)(u / ntiles), tb = (int)(u % ntiles);
+      const int te = (int)min((int64_t)ntiles, tb + (u_end - u));
+      // every wave is done with the previous piece's LDS stages and scales
+      if (piece) __syncthreads();
+      wide_piece<DT, DP, true>(p, lds, ks_l, p.dp_blocks + qi, tb, te, 2 * blk + piece);
+      u += te - tb;
+    }
   }
 }
 #undef DC_ATTN_WAIT_VMCNT
@@ -1232,11 +1283,10 @@ static AttnPlan attn_plan_dp(int dtype, int B, int H, int Lq, int Lk) {
   const int slots = dtype == DC_BF16 ? attn_slots<DC_BF16, DP>() : attn_slots<DC_F16, DP>();
   AttnPlan pl = attn_plan(qtiles, ntiles, slots);
   if constexpr (DP == 64) {
-    // at Dp = 64 attn_wide_kernel runs the same whole 128-row query tiles
-    // (two workgroups per CU, like attn_kernel); plans with a stream-K split
-    // keep attn_kernel
+    // at Dp = 64 attn_wide_kernel runs the same 128-row query tiles and
+    // stream-K pieces as attn_kernel (two workgroups per CU)
     static_assert(Wide<64>::BQW == BQ, "the Dp = 64 wide tiles are attn_kernel's query tiles");
-    if (wide_ok && pl.sk_blocks == 0) pl.wide = true;
+    if (wide_ok) pl.wide = true;
   }
   return pl;
 }
@@ -1272,11 +1322,13 @@ static int launch_attn(AttnArgs& a, hipStream_t st) {
                      0, st, a);
   if (int e = launch_status("kquant_kernel")) return e;
   if (a.wide) {
-    hipLaunchKernelGGL((attn_wide_kernel<DT, DP>), dim3((unsigned)a.dp_blocks), dim3(Wide<DP>::NT), 0, st, a);
-    return launch_status("attn_wide_kernel");
+    hipLaunchKernelGGL((attn_wide_kernel<DT, DP>), dim3((unsigned)(a.dp_blocks + a.sk_blocks)), dim3(Wide<DP>::NT), 0,
+                       st, a);
+    if (int e = launch_status("attn_wide_kernel")) return e;
+  } else {
+    hipLaunchKernelGGL((attn_kernel<DT, DP>), dim3((unsigned)(a.dp_blocks + a.sk_blocks)), dim3(256), 0, st, a);
+    if (int e = launch_status("attn_kernel")) return e;
   }
-  hipLaunchKernelGGL((attn_kernel<DT, DP>), dim3((unsigned)(a.dp_blocks + a.sk_blocks)), dim3(256), 0, st, a);
-  if (int e = launch_status("attn_kernel")) return e;
   if (a.sk_blocks == 0) return DC_OK;
   hipLaunchKernelGGL((attn_merge_kernel<DT, DP>), dim3((unsigned)a.sk_tiles), dim3(256), 0, st, a);
   return launch_status("attn_merge_kernel");
