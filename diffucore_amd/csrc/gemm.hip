@@ -472,6 +472,81 @@ __device__ __forceinline__ void store_tile_lds(const v16i (&acc)[4][4], const Ge
   }
 }
 
+// Epilogue of one wave's full (32 FN) n x (32 FM) m block through LDS, for the
+// register-staged kernel: the wave's outputs go to its own WAVE_BYTES of the
+// LDS stages (free after the main loop), row m at a pitch of its bytes plus
+// 16 (the padding spreads a 16-byte write of 16 consecutive rows over all
+// banks), JP 32-row m blocks per pass; then each row leaves as one contiguous
+// run, 16 bytes per lane. Stored from the MFMA layout instead, one
+// instruction writes 16 or 32 bytes into each of 32 rows. Same rounding as
+// store_tile. A lane reads back what other lanes of its wave wrote: the
+// wavefront fences and barrier keep the compiler from moving LDS accesses
+// across.
+template <int OUT_DT, int BIAS_DT, int FN, int FM, int WAVE_BYTES>
+__device__ __forceinline__ void store_tile_staged(const v16i (&acc)[FN][FM], const GemmArgs& p, int m0, int n0, int nb,
+                                                  int mb, const float* sw_l, const float* b_l, const float* sx_l,
+                                                  int hf, int l32, int lane, uint8_t* stage) {
+  constexpr int OB = (OUT_DT == DC_F16 || OUT_DT == DC_BF16) ? 2 : 4;
+  constexpr int ROWB = 32 * FN * OB;   // output row bytes of the block
+  constexpr int RP = ROWB + 16;        // staged row pitch
+  constexpr int CH = ROWB / 16;        // 16-byte chunks per row
+  constexpr int JP = (FM % 2 == 0 && 64 * RP <= WAVE_BYTES) ? 2 : 1;   // 32-row m blocks per pass
+  constexpr int NIT = 32 * JP * CH / 64;                              // store instructions per pass
+  static_assert(32 * RP <= WAVE_BYTES, "one 32-row block must fit the wave's LDS share");
+  static_assert((32 * JP * CH) % 64 == 0, "a pass must be whole store instructions");
+  constexpr bool HB = BIAS_DT != DC_NONE;
+  float sxm[FM];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) sxm[j] = OUT_DT != DC_I32 ? sx_l[mb + 32 * j + l32] : 0.0f;
+#pragma unroll
+  for (int j0 = 0; j0 < FM; j0 += JP) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nl = nb + 32 * i + 8 * g + 4 * hf;
+        float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (OUT_DT != DC_I32) s4 = *reinterpret_cast<const float4*>(sw_l + nl);
+        if constexpr (HB) b4 = *reinterpret_cast<const float4*>(b_l + nl);
+#pragma unroll
+        for (int jj = 0; jj < JP; ++jj) {
+          const int j = j0 + jj;
+          uint8_t* row = stage + (32 * jj + l32) * RP;
+          const int av[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          if constexpr (OUT_DT == DC_I32) {
+            *reinterpret_cast<int4*>(row + 16 * (8 * i + 2 * g + hf)) = make_int4(av[0], av[1], av[2], av[3]);
+          } else if constexpr (OUT_DT == DC_F32) {
+            const float y0 = epi_pre<OUT_DT, HB>(av[0], sxm[j], s4.x, b4.x);
+            const float y1 = epi_pre<OUT_DT, HB>(av[1], sxm[j], s4.y, b4.y);
+            const float y2 = epi_pre<OUT_DT, HB>(av[2], sxm[j], s4.z, b4.z);
+            const float y3 = epi_pre<OUT_DT, HB>(av[3], sxm[j], s4.w, b4.w);
+            *reinterpret_cast<float4*>(row + 16 * (8 * i + 2 * g + hf)) = make_float4(y0, y1, y2, y3);
+          } else {
+            const uint32_t lo = epi_pair<OUT_DT, HB>(av[0], av[1], sxm[j], s4.x, s4.y, b4.x, b4.y);
+            const uint32_t hi = epi_pair<OUT_DT, HB>(av[2], av[3], sxm[j], s4.z, s4.w, b4.z, b4.w);
+            *reinterpret_cast<uint2*>(row + 16 * (4 * i + g) + 8 * hf) = make_uint2(lo, hi);
+          }
+        }
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int k = 0; k < NIT; ++k) {
+      const int idx = 64 * k + lane, r = idx / CH, c = idx % CH;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * RP + 16 * c);
+      const int64_t m = m0 + mb + 32 * j0 + r;
+      *reinterpret_cast<uint4*>(static_cast<uint8_t*>(p.out) + (m * p.ldo + n0 + nb) * OB + 16 * c) = v;
+    }
+    if (j0 + JP < FM) {
+      // the next pass overwrites what this one read back
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+}
+
 template <class T, int OUT_DT, int BIAS_DT>
 __global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
   constexpr int FN = T::FN, FM = T::FM, NT = T::NT;
@@ -640,8 +715,14 @@ __global__ void __launch_bounds__(T::NT, 1) w8a8_gemm_kernel(GemmArgs p) {
 #undef GEMM_STORE
 #undef GEMM_FRAGS
 
-  // epilogue: acc[i][j] register r -> n = n0 + nb + 32 i + 8 (r / 4) + 4 hf + r % 4, m = m0 + mb + 32 j + l32
-  store_tile<OUT_DT, BIAS_DT, FN, FM>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l, hf, l32);
+  // epilogue: acc[i][j] register r -> n = n0 + nb + 32 i + 8 (r / 4) + 4 hf + r % 4, m = m0 + mb + 32 j + l32;
+  // whole tiles through the (now free) LDS stages, each wave in its own share
+  constexpr int WAVE_BYTES = 2 * STAGE / (T::WN * T::WM) / 16 * 16;
+  if (p.vec16 && m0 + BM <= p.M && n0 + BN <= p.N)
+    store_tile_staged<OUT_DT, BIAS_DT, FN, FM, WAVE_BYTES>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, sw_l, b_l,
+                                                           sx_l, hf, l32, lane, smem + wv * WAVE_BYTES);
+  else
+    store_tile<OUT_DT, BIAS_DT, FN, FM>(acc, p, m0, n0, wn * 32 * FN, wm * 32 * FM, BM, BN, sw_l, b_l, sx_l, hf, l32);
 }
 
 // ---------------------------------------------------------------- DMA-fed kernel
@@ -941,7 +1022,9 @@ static int device_cus() {
 // 256 x 256 (2.25 rounds on 256 CUs) but exactly 768 of 192 x 256. The
 // 128 x 128 tiles lose less to their prologue and epilogue the shorter K is:
 // measured on the SD1.5 / SDXL / FLUX shapes, they match or beat the larger
-// tiles at equal fill below K = 3072 (0.9) and reach 0.7 of them beyond.
+// tiles at equal fill below K = 3072 when they take one round (0.9), reach
+// 0.75 of them over several rounds (SDXL's 8192 x 640 -> 5120: 51.7 us
+// against 48.2 us for 256 x 256 tiles) and 0.7 at K = 3072 and beyond.
 // 192 (n) x 128 (m) on 4 waves (1 per CU; 0.8) serves the problems whose
 // 128 x 128 tiles would put two workgroups on some CUs and one on others,
 // and is a candidate only when its own tiles cover at least 3/4 of the CUs
@@ -952,9 +1035,10 @@ static int device_cus() {
 // Kernel plan for a problem: DC_GEMM_PLAN_* (the choice pick_tile launches).
 static int plan_tile(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
   struct Cand { int bn, bm, per_cu; float eff; };
-  const Cand cands[4] = {{256, 256, 1, 1.0f}, {192, 256, 1, 0.95f}, {128, 128, 2, K < 3072 ? 0.9f : 0.7f},
-                         {192, 128, 1, 0.8f}};
   const int cus = device_cus();
+  const bool one_round_128 = ((M + 127) / 128) * ((N + 127) / 128) <= 2 * (int64_t)cus;
+  const Cand cands[4] = {{256, 256, 1, 1.0f}, {192, 256, 1, 0.95f},
+                         {128, 128, 2, K >= 3072 ? 0.7f : one_round_128 ? 0.9f : 0.75f}, {192, 128, 1, 0.8f}};
   int best = 0;
   float best_score = -1.0f;
   for (int i = 0; i < 4; ++i) {

@@ -412,8 +412,8 @@ def test_gemm_plan_choice_without_a_gpu():
     answers). FLUX-step shapes take the DMA-fed 256x256 kernel when K is a
     multiple of 256, the 192x256 tiles when they fill the last round better,
     192x128 tiles (one per CU) for the 512-row text qkv / MLP up whose 128x128
-    tiles would load CUs unevenly, and 2-per-CU 128x128 tiles for the shorter
-    ones."""
+    tiles would load CUs unevenly, 2-per-CU 128x128 tiles for the shorter
+    ones when they fit one round, and 256x256 tiles over several."""
     so = _lib.lib()
     assert so.dc_w8a8_gemm_plan(4608, 21504, 3072, 3072, 3072) == 3      # linear1
     assert so.dc_w8a8_gemm_plan(4608, 3072, 15360, 15360, 15360) == 3    # linear2
@@ -422,6 +422,7 @@ def test_gemm_plan_choice_without_a_gpu():
     assert so.dc_w8a8_gemm_plan(512, 12288, 3072, 3072, 3072) == 4       # text MLP up
     assert so.dc_w8a8_gemm_plan(512, 3072, 3072, 3072, 3072) == 2        # text proj (64 tiles of 192x128)
     assert so.dc_w8a8_gemm_plan(2048, 1280, 1280, 1280, 1280) == 2       # SDXL level-2 q/k/v/o
+    assert so.dc_w8a8_gemm_plan(8192, 5120, 640, 640, 640) == 0          # SDXL GEGLU: 5 rounds of 128x128 lose
     assert so.dc_w8a8_gemm_plan(4096, 12288, 272, 272, 272) == 0         # K % 256 != 0
     assert so.dc_w8a8_gemm_plan(0, 1, 16, 16, 16) == -1                  # invalid shape
     assert [_int8.gemm_plan(4608, 21504, 3072), _int8.gemm_plan(512, 9216, 3072)] == ["dma_256x256", "192x128"]
