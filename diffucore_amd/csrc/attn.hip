@@ -1081,17 +1081,20 @@ __device__ __forceinline__ void wide_piece(const AttnArgs& p, uint8_t* lds, floa
     float ts = 0.f;
     qk_mfma<DP>(ka, qf, magic, nxt);
     softmax_exp<DT, TAIL>(cur, key0, p.Lk, c, __builtin_fmaf(MAGIC_F, c, m), ts, pk);
-    // 56 of the ~96 VALU instructions of the exponentials first (the K
+    // UP of the ~96 VALU instructions of the exponentials first (the K
     // operand reads issued after the barrier land meanwhile, so the first
     // QK^T MFMA of tile + 1 does not hold up the in-order issue), then the
     // 2 ND MFMAs with the rest spread behind them. Measured at FLUX against
     // one MFMA then 12 VALU from the start: 2.7% faster per call, same bits;
-    // 48 to 72 up front measure alike, all of it up front is slower.
-    __builtin_amdgcn_sched_group_barrier(0x002, 56, 0);
+    // 48 to 72 up front measure alike, all of it up front is slower. At
+    // Dp = 64 (4 QK^T MFMAs) 72 up front measured 1.5% faster than 56 on
+    // SD1.5's shape (40 alike; 24 and 96 slower).
+    constexpr int UP = DP == 128 ? 56 : 72;
+    __builtin_amdgcn_sched_group_barrier(0x002, UP, 0);
 #pragma unroll
     for (int z = 0; z < 2 * ND; ++z) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 40 / (2 * ND), 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, (96 - UP) / (2 * ND), 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     lazy_fixup<DT, DP, TAIL>(cur, key0, p.Lk, c, m, lsum, ts, o, pk);
