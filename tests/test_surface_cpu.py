@@ -423,6 +423,7 @@ def test_gemm_plan_choice_without_a_gpu():
     assert so.dc_w8a8_gemm_plan(512, 3072, 3072, 3072, 3072) == 2        # text proj (64 tiles of 192x128)
     assert so.dc_w8a8_gemm_plan(2048, 1280, 1280, 1280, 1280) == 2       # SDXL level-2 q/k/v/o
     assert so.dc_w8a8_gemm_plan(8192, 5120, 640, 640, 640) == 0          # SDXL GEGLU: 5 rounds of 128x128 lose
+    assert so.dc_w8a8_gemm_plan(8192, 640, 640, 640, 640) == 2           # SDXL q/k/v/o: 192x128 would pad N by 20%
     assert so.dc_w8a8_gemm_plan(4096, 12288, 272, 272, 272) == 0         # K % 256 != 0
     assert so.dc_w8a8_gemm_plan(0, 1, 16, 16, 16) == -1                  # invalid shape
     assert [_int8.gemm_plan(4608, 21504, 3072), _int8.gemm_plan(512, 9216, 3072)] == ["dma_256x256", "192x128"]
