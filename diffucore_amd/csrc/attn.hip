@@ -135,20 +135,23 @@ __global__ void __launch_bounds__(256) kstats_kernel(AttnArgs p) {
   }
   // The 16 row groups' partial sums, then each channel's 16 partials added in
   // row-group order. Row group rg keeps channels 8 ch + 0..3 at float
-  // 4 ch + 0..3 and 8 ch + 4..7 at 96 + 4 ch + 0..3 of its 160-float row: the
-  // 16 lanes of one row group write 256 contiguous bytes per half, and the 64
-  // channels a wave reads fall in distinct banks, so neither side conflicts.
-  __shared__ __attribute__((aligned(16))) float red[16 * 160];
+  // 4 ch + 0..3 and 8 ch + 4..7 at 96 + 4 ch + 0..3 of its row of RP floats:
+  // the 16 lanes of one row group write 256 contiguous bytes per half. A read
+  // instruction takes two rows (ds_read2_b32), and 32 lanes' channels sit on
+  // 32 banks of a row; RP = 16 (mod 64) puts the next row's copies on the
+  // other 32 (a 160-float pitch, 32 mod 64, put them on the same ones).
+  constexpr int RP = 208;
+  __shared__ __attribute__((aligned(16))) float red[16 * RP];
   if (ch * 8 < p.D) {
-    *reinterpret_cast<float4*>(red + rg * 160 + 4 * ch) = make_float4(ak[0], ak[1], ak[2], ak[3]);
-    *reinterpret_cast<float4*>(red + rg * 160 + 96 + 4 * ch) = make_float4(ak[4], ak[5], ak[6], ak[7]);
+    *reinterpret_cast<float4*>(red + rg * RP + 4 * ch) = make_float4(ak[0], ak[1], ak[2], ak[3]);
+    *reinterpret_cast<float4*>(red + rg * RP + 96 + 4 * ch) = make_float4(ak[4], ak[5], ak[6], ak[7]);
   }
   __syncthreads();
   if (t < p.D) {
     const int idx = ((t & 4) ? 96 : 0) + 4 * (t >> 3) + (t & 3);
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s += red[i * 160 + idx];
+    for (int i = 0; i < 16; ++i) s += red[i * RP + idx];
     p.kpart[((int64_t)(b * p.H + h) * p.nwin + w) * p.D + t] = s;
   }
 }
@@ -172,7 +175,10 @@ __global__ void __launch_bounds__(256) kquant_kernel(AttnArgs p) {
   const int bh = b * p.H + h, t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int nblk = p.Lk64 / BKEY;
   const int blk = KQ_BLOCKS * g + wv;
-  __shared__ __attribute__((aligned(16))) float ksum_s[128];
+  // the window sums, 4 floats of padding after channel 63: the float4 reads
+  // of the lanes' 16-channel slices then fall in distinct banks (channel 64 c
+  // would share a bank with channel 0 unpadded)
+  __shared__ __attribute__((aligned(16))) float ksum_s[128 + 4];
 
   // the block's key loads first (clamped in bounds: a wave past the last
   // block reads it again, rows past Lk read row Lk - 1, chunks past D the last
@@ -202,7 +208,7 @@ __global__ void __launch_bounds__(256) kquant_kernel(AttnArgs p) {
       for (int i = 0; i < 16; ++i)
         if (w0 + i < p.nwin) s += part[i];
     }
-    ksum_s[t] = s;
+    ksum_s[t + 4 * (t >> 6)] = s;
     if (g == 0) p.ksum[(int64_t)bh * p.D + t] = s;
   }
   __syncthreads();
@@ -214,8 +220,9 @@ __global__ void __launch_bounds__(256) kquant_kernel(AttnArgs p) {
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
     const bool in = hh ? in1 : in0;
-    const float4 a = in ? *reinterpret_cast<const float4*>(ksum_s + 16 * cp + 8 * hh) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4 c = in ? *reinterpret_cast<const float4*>(ksum_s + 16 * cp + 8 * hh + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int c0 = 16 * cp + 8 * hh, c1 = c0 + 4;   // channel groups of 4, padded index below
+    const float4 a = in ? *reinterpret_cast<const float4*>(ksum_s + c0 + 4 * (c0 >> 6)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 c = in ? *reinterpret_cast<const float4*>(ksum_s + c1 + 4 * (c1 >> 6)) : make_float4(0.f, 0.f, 0.f, 0.f);
     km[8 * hh] = a.x; km[8 * hh + 1] = a.y; km[8 * hh + 2] = a.z; km[8 * hh + 3] = a.w;
     km[8 * hh + 4] = c.x; km[8 * hh + 5] = c.y; km[8 * hh + 6] = c.z; km[8 * hh + 7] = c.w;
   }
