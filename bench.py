@@ -718,10 +718,22 @@ def shapes_report(dev):
             qb = UB.to_int8(copy.deepcopy(blk), dev)
             ms_q = per_call_ms(lambda: qb(x, ctx))
             out = qb(x, ctx) - x
+            # device time without the modules' Python and launch cost: the block captured in a HIP graph
+            # (None if a module's ops cannot be captured)
+            try:
+                gms_e = graph_call_ms(lambda: blk(x, ctx), reps=5)
+                gms_q = graph_call_ms(lambda: qb(x, ctx), reps=5)
+            except RuntimeError as e:
+                print(f"[bench] unet block {lv.name}: graph capture failed: {e}", file=sys.stderr, flush=True)
+                gms_e = gms_q = None
         print(json.dumps({"kind": "unet_block", "shape": lv.name, "B": lv.batch, "tokens": lv.tokens, "dim": lv.dim,
                           "heads": lv.heads, "ctx": [lv.ctx_len, lv.ctx_dim], "dtype": "float16",
                           "fp16_eager_ms": round(ms_e, 4), "int8_ms": round(ms_q, 4),
-                          "speedup": round(ms_e / ms_q, 2), "update_vs_fp16": _cmp(out, ref)}), flush=True)
+                          "speedup": round(ms_e / ms_q, 2),
+                          "fp16_graph_ms": round(gms_e, 4) if gms_e else None,
+                          "int8_graph_ms": round(gms_q, 4) if gms_q else None,
+                          "graph_speedup": round(gms_e / gms_q, 2) if gms_e and gms_q else None,
+                          "update_vs_fp16": _cmp(out, ref)}), flush=True)
         del blk, qb, x, ctx, ref, out
     # QK RMSNorm + rotary (dc_qk_norm_rope) against FLUX's eager ops, at the FLUX double-block shape:
     # txt (512) and img (4096) q/k/v views of the two qkv projections -> joint (B, H, L, D) q, k, v
