@@ -1221,9 +1221,10 @@ static int attn_slots() {
   if (!n) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&attn_kernel<DT, DP>),
-                                                     256, 0) != hipSuccess || per_cu <= 0)
-      per_cu = 2;
+    // the kernel that runs the 128-query tiles: attn_wide_kernel at Dp = 64, attn_kernel at 128
+    const void* fn = DP == 64 ? reinterpret_cast<const void*>(&attn_wide_kernel<DT, 64>)
+                              : reinterpret_cast<const void*>(&attn_kernel<DT, DP>);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu <= 0) per_cu = 2;
     n = cus * per_cu;
     slots[dev].store(n, std::memory_order_relaxed);
   }
