@@ -231,11 +231,12 @@ def _gemm_unsplit(q, w, sx, sw, bias, dtype):
 
 
 @pytest.mark.parametrize("mnk", [(512, 3072, 12288), (512, 3072, 3072), (154, 640, 4096), (77, 1280, 4096),
-                                 (300, 520, 8192)])
+                                 (300, 520, 8192), (154, 1280, 2048), (77, 640, 2048)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_split_k_is_bit_identical(gpu, mnk, dtype):
     """Small-M, long-K problems split k over workgroups into int32 partials
-    (the FLUX text MLP down, SDXL cross-attention k/v, ...); the epilogue over
+    (the FLUX text MLP down, SDXL's 154-row cross-attention k/v at K = 2048,
+    ...); the epilogue over
     their exact sum equals the unsplit GEMM and the oracle bit for bit."""
     from diffucore_amd import _lib
     m, n, k = mnk

@@ -282,6 +282,8 @@ def test_argument_checks_fail_before_any_launch():
     # split-K workspace: small M with long K splits (FLUX text MLP down: 4 slices of int32 partials), big M does not
     assert so.dc_w8a8_gemm_workspace_bytes(512, 3072, 12288, 12288, 12288) == 4 * 512 * 3072 * 4
     assert so.dc_w8a8_gemm_workspace_bytes(4096, 3072, 12288, 12288, 12288) == 0
+    assert so.dc_w8a8_gemm_workspace_bytes(154, 1280, 2048, 2048, 2048) == 4 * 154 * 1280 * 4   # 20 tiles
+    assert so.dc_w8a8_gemm_workspace_bytes(512, 3072, 2048, 2048, 2048) == 0   # 96 tiles: no 2048-deep split
     assert so.dc_w8a8_gemm_workspace_bytes(512, 3072, 100, 112, 112) == 0
     assert so.dc_int8_attn_workspace_bytes(1, 24, 4608, 4608, 128) > 24 * 4608 * 128
     assert so.dc_int8_attn_workspace_bytes(1, 1, 1, 1, 200) == 0
