@@ -9,8 +9,11 @@ Covered: the quantize kernel, each GEMM plan the FLUX step uses (DMA-fed
 256 x 256, 192 x 128 at the text MLP-up shape, 192 x 256 / 128 x 128,
 split-K with its workspace and epilogue pass, a grouped launch of two
 layers, the same pair with the gated residual epilogue) and the INT8 attention (K statistics, K quantize, attention): the
-256-query kernel at the FLUX shape, stream-K pieces and their merge at SDXL's
-4096-token self-attention, and the 128-query kernel whole.
+DMA-fed kernel with 256-query tiles at the FLUX shape, with 128-query tiles
+and stream-K pieces plus their merge at SDXL's 4096-token self-attention and
+with whole 128-query tiles at head dim 64, and the register-staged 128-query
+kernel on a head-dim-128 grid too small for 256-query tiles, stream-K pieces
+included.
 """
 
 from __future__ import annotations
@@ -30,7 +33,7 @@ BF16 = torch.bfloat16
 LINEARS = [(4096, 512, 4096), (512, 3072, 3072), (512, 3072, 12288), (1000, 768, 1280), (1024, 512, 1024),
            (300, 512, 1024)]
 NS = len(LINEARS) - 2   # the layers called one by one
-ATTN = [(1, 24, 4608, 128), (2, 10, 4096, 64), (1, 4, 1000, 64)]
+ATTN = [(1, 24, 4608, 128), (2, 10, 4096, 64), (1, 4, 1000, 64), (1, 4, 4096, 128)]
 
 
 def _case(gpu, seed):
