@@ -30,11 +30,22 @@ The same run also measures, and adds to the JSON line:
   * the MFMA-only throughput this device sustains (dc_mfma_probe), next to
     the published peak in the roofline object.
 
+Benchmark configs (the shapes --shapes and --cpu-configs cover):
+  1. a W8A8 linear on x fp32 [8192, 320] with outlier channels, W [1280, 320],
+     group 0, fp32 out (the reference's CPU-runnable case);
+  2. SD1.5 at 512^2: self-attention 2 x 8 x 4096 (D 40), cross-attention over
+     77 context tokens, the transformer block's W8A8 linears;
+  3. SDXL at 1024^2: self-attention 2 x 10 x 4096 and 2 x 20 x 1024 (D 64),
+     cross-attention, the block's linears;
+  4. FLUX.1 at 1024^2, per call: joint attention 1 x 24 x 4608 (D 128, bf16)
+     and every W8A8 linear shape;
+  5. one FLUX.1-schnell denoise step (the hot path above, and flux_step.py).
+
     python bench.py [--steps K] [--warmup W] [--no-full] [--no-cpu]
     python bench.py --copy-calibration   # 1 GiB device copy for counter scaling
     python bench.py --cpu-configs        # the reference's CPU path at every config shape (host cores only)
     python bench.py --mfma-ceiling       # MFMA-only throughput (int8, bf16)
-    python bench.py --shapes             # per-shape report for every BASELINE config (+ the GEMM A/B)
+    python bench.py --shapes             # per-shape report for every benchmark config (+ the GEMM A/B)
     python bench.py --gemm-ab            # same-process GEMM A/B against torch._int_mm (hipBLASLt)
 """
 
@@ -348,7 +359,7 @@ def traffic_summary(root: Path) -> None:
 
 
 def cpu_cfg1(budget_s: float = 4.0):
-    """BASELINE config 1 on the reference's CPU path: W8A8 linear on x fp32
+    """Benchmark config 1 on the reference's CPU path: W8A8 linear on x fp32
     [8192, 320] ~N(0, 1) with 2 of 320 channels (0.5%) scaled x20 as outliers,
     W [1280, 320] ~N(0, 0.02), per-token int8 activations, per-channel int8
     weights, group 0, int32 accumulate, fp32 out, seed 0 (generator draws:
@@ -378,7 +389,7 @@ def cpu_cfg1(budget_s: float = 4.0):
 def cpu_configs(budget_s: float = 2.0) -> None:
     """The reference's CPU path (oracle/cpu_path.py: the W8A8 linear as
     quantize_rows(rotate(x)) -> torch._int_mm -> rescale; attention as fp32
-    SDPA, where the int8 backend falls through on CPU) at each BASELINE config
+    SDPA, where the int8 backend falls through on CPU) at each benchmark config
     shape, on all host threads. Each shape runs on a sample of its rows or
     queries (all keys, all heads) for about ``budget_s`` and is scaled to the
     full call by its share of the work; one JSON line per shape."""
@@ -572,7 +583,7 @@ def _cmp(y, ref):
 
 
 def shapes_report(dev):
-    """One JSON line per BASELINE config shape: time, TOPS, % of peak, accuracy."""
+    """One JSON line per benchmark config shape: time, TOPS, % of peak, accuracy."""
     import torch.nn.functional as F
     from diffucore_amd import Int8Linear, attention_bhld, quantize_activation
     from diffucore_amd._attention import SHORT_KEYS
@@ -789,7 +800,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (scales the rocprofv3 byte counters) and exit")
     ap.add_argument("--shapes", action="store_true",
-                    help="only print the per-shape report (every BASELINE config shape) and exit")
+                    help="only print the per-shape report (every benchmark config shape) and exit")
     ap.add_argument("--gemm-ab", action="store_true",
                     help="only print the same-process GEMM A/B against torch._int_mm (hipBLASLt) at FLUX's "
                          "linear shapes and exit")
@@ -797,7 +808,7 @@ def main():
                     help="only measure the MFMA-only throughput of the device (int8 and bf16, 1 and 2 waves per "
                          "SIMD, constant and changing operands) and exit")
     ap.add_argument("--cpu-configs", action="store_true",
-                    help="only time the reference's CPU path at every BASELINE config shape (bounded row / query "
+                    help="only time the reference's CPU path at every benchmark config shape (bounded row / query "
                          "samples scaled to a full call, all host threads) and exit (no GPU)")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="only summarize rocprofv3 FETCH_SIZE / WRITE_SIZE runs under DIR (copy_* and step_*) "

@@ -1,4 +1,4 @@
-"""The full synthetic FLUX.1-schnell denoise step on the
+"""The full synthetic FLUX.1-schnell denoise step (benchmark config 5) on the
 GPU: the DiT of ``flux_step.py`` (a restatement of the reference's
 ``flux_dit.py:254-447``) at full width and full token count (hidden 3072,
 24 heads, 4096 image + 512 text tokens) with reduced depth (2 double + 2
@@ -131,7 +131,7 @@ def test_int8_step_is_deterministic(flux):
 
 
 def test_full_depth_latent_against_bf16(gpu):
-    """BASELINE config 5 at full depth (19 double + 38 single blocks, the
+    """Benchmark config 5 at full depth (19 double + 38 single blocks, the
     bench's seeds): the 4-step schnell latent of the INT8 step (W8A8 block
     linears, INT8 attention, fused glue) against the bf16 eager step, within
     rel L2 <= 0.035 and cosine >= 0.9995 (measured 0.025 and 0.9997)."""

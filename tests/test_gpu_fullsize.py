@@ -1,4 +1,4 @@
-"""The hot path at BASELINE.json's full shapes, through properties that hold
+"""The hot path at the benchmark's full shapes, through properties that hold
 at any size (the oracle covers smaller sizes bit for bit):
 
 * int32 GEMM: row and column checksums against exact int64 identities,

@@ -101,7 +101,7 @@ def test_int8_linear_matches_oracle_and_float(gpu, k, n, group):
 
 
 def test_cfg1_sd15_linear_exact(gpu):
-    """BASELINE config 1 itself, seeded as specified: x fp32 [8192, 320] ~N(0, 1)
+    """Benchmark config 1 itself, seeded as specified: x fp32 [8192, 320] ~N(0, 1)
     with 0.5% of its channels (2 of 320) scaled x20, W [1280, 320] ~N(0, 0.02),
     group 0, fp32 out, through ``Int8Linear.forward``. The weight codes and
     scales (quantized on the CPU) equal the oracle's weight quantizer; the

@@ -1,4 +1,4 @@
-"""The drop-in inside an SD1.5 / SDXL UNet transformer block (BASELINE
+"""The drop-in inside an SD1.5 / SDXL UNet transformer block (benchmark
 configs 2 and 3) on the GPU: the reference's BasicTransformerBlock
 (``unet.py:122-183``, restated in ``unet_block.py``) at the config shapes,
 batch 2, fp16, with every linear swapped for W8A8 by ``quantize_linears`` and

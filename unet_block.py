@@ -1,5 +1,5 @@
 """Synthetic SD1.5 / SDXL UNet transformer block for measuring the hot path in
-place (BASELINE configs 2 and 3).
+place (the SD1.5 and SDXL benchmark configs).
 
 Restates the reference's ``CrossAttention``, ``GEGLU``, ``FeedForward`` and
 ``BasicTransformerBlock`` (``src/diffucore/models/unet.py:122-183``): self-
@@ -43,8 +43,8 @@ class UNetLevel:
     batch: int = 2
 
 
-# SD1.5 at 512^2, the first (highest-resolution) level;
-# config 3: SDXL at 1024^2, its two transformer levels
+# the SD1.5 config: 512^2, the first (highest-resolution) level;
+# the SDXL config: 1024^2, its two transformer levels
 SD15_L1 = UNetLevel("sd15_l1", 320, 8, 4096, 768)
 SDXL_L1 = UNetLevel("sdxl_l1", 640, 10, 4096, 2048)
 SDXL_L2 = UNetLevel("sdxl_l2", 1280, 20, 1024, 2048)
@@ -122,7 +122,7 @@ class BasicTransformerBlock(nn.Module):
 
 def linear_names(block: BasicTransformerBlock) -> list[str]:
     """The block's linears a W8A8 swap replaces: q/k/v/out of both attentions
-    and the GEGLU feed-forward's two."""
+    and the GEGLU feed-forward's two (the SDXL config)."""
     names = []
     for a in ("attn1", "attn2"):
         names += [f"{a}.to_q", f"{a}.to_k", f"{a}.to_v", f"{a}.to_out.0"]
