@@ -123,6 +123,24 @@ def test_codes_and_scales_bit_exact(gpu, B, Lq, Lk, H, D, dtype):
     assert np.array_equal(qs[:, :, :Lq].cpu().numpy().view(np.uint32), qs_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("B,H,Lk,D,dtype", [
+    # the FLUX key set; 469 windows summed into one head's ksum; 5160 windows
+    # over 40 heads with a ragged last window at head dim 64
+    (1, 24, 4608, 128, torch.bfloat16), (1, 1, 60000, 128, torch.float16),
+    (1, 40, 16421, 64, torch.float16),
+])
+def test_k_preparation_large_key_sets_bit_exact(gpu, B, H, Lk, D, dtype):
+    print(f"[attn] K preparation B {B} H {H} Lk {Lk} D {D} {DT[dtype]}", flush=True)
+    q, k, v = _inputs(B, 64, Lk, H, D, dtype, seed=5)
+    _, ws = _run(q, k, v, gpu)
+    ksum = OA.k_colsum(np32(k))
+    assert np.array_equal(ws["ksum"].cpu().numpy().view(np.uint32), ksum.view(np.uint32))
+    ki, ks = OA.k_quantize(np32(k), ksum)
+    assert np.array_equal(ws["ks"].cpu().numpy().view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(ws["k8"][..., :D].cpu().numpy(), ki)
+    assert not ws["k8"][..., D:].any()
+
+
 @pytest.mark.parametrize("B,Lq,Lk,H,D,dtype", CASES)
 def test_output_close_to_oracle_and_sdpa(gpu, B, Lq, Lk, H, D, dtype):
     q, k, v = _inputs(B, Lq, Lk, H, D, dtype)
