@@ -797,6 +797,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-full", action="store_true", help="skip the full FLUX step vs bf16 comparison")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--compiled-bf16", action="store_true",
+                    help="also time the bf16 step under torch.compile (inductor; compile time excluded)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (scales the rocprofv3 byte counters) and exit")
     ap.add_argument("--shapes", action="store_true",
@@ -863,6 +865,19 @@ def main():
         with torch.no_grad():
             bf16_glue_ms = time_steps(lambda: model(x0, txt, sigmas[:1].to(x0.dtype), y, pe), 3, 1)
         set_fused_glue(model, False)
+        if args.compiled_bf16:
+            # the strongest bf16 baseline this image builds: the same eager ops
+            # fused by inductor's generated kernels
+            log("full step, bf16 under torch.compile: compiling")
+            compiled = torch.compile(model)
+            with torch.no_grad():
+                t0 = time.perf_counter()
+                compiled(x0, txt, sigmas[:1].to(x0.dtype), y, pe)
+                torch.cuda.synchronize()
+                log(f"full step, bf16 under torch.compile: compiled in {time.perf_counter() - t0:.0f} s; timing")
+                bf16_compiled_ms = time_steps(lambda: compiled(x0, txt, sigmas[:1].to(x0.dtype), y, pe), 3, 1)
+            del compiled
+            torch._dynamo.reset()
     log("quantizing block linears to W8A8 (ConvRot group 256), stamping int8_turing")
     names = FS.block_linear_names(model)
     quantize_linears(model, names, dev, 256)
@@ -878,13 +893,17 @@ def main():
         extra["denoise_step"] = {
             "int8_ms": round(int8_ms, 3), "bf16_ms": round(bf16_ms, 3), "speedup": round(bf16_ms / int8_ms, 3),
             "bf16_fused_glue_ms": round(bf16_glue_ms, 3),
+            **({"bf16_compiled_ms": round(bf16_compiled_ms, 3), "speedup_vs_compiled": round(bf16_compiled_ms / int8_ms, 3)}
+               if args.compiled_bf16 else {}),
             "latent_rel_l2_vs_bf16": round(float((a - b).norm() / b.norm()), 5),
             "latent_cos_vs_bf16": round(float(a @ b / (a.norm() * b.norm())), 6),
             "what": "full synthetic FLUX.1-schnell forward + euler update at 1024^2 (flux_step.py), "
                     "4-step final latent compared; int8 = W8A8 linears + INT8 attention + fused glue "
                     "(LayerNorm-modulate/GELU quantize passes, QK norm + rotary, gate + residual in the GEMM "
                     "epilogue); bf16 = the reference's "
-                    "eager ops, bf16_fused_glue = bf16 with only the QK norm + rotary pass fused",
+                    "eager ops, bf16_fused_glue = bf16 with only the QK norm + rotary pass fused"
+                    + (", bf16_compiled = the eager bf16 model under torch.compile (inductor)" if args.compiled_bf16
+                       else ""),
         }
         log(f"full step: int8 {int8_ms:.2f} ms vs bf16 {bf16_ms:.2f} ms")
 
