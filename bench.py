@@ -488,6 +488,43 @@ def per_call_ms(fn, reps: int = 20) -> float:
     return t[reps // 2]
 
 
+def unet_compiled(dev):
+    """The UNet transformer block (unet_block.py) at SD1.5 / SDXL shapes:
+    fp16 eager, the fp16 block under torch.compile (inductor; compile time
+    excluded) and the W8A8 + INT8 block, per call (HIP events around each
+    call, launch cost included) and as device time (the block captured in a
+    HIP graph; None where capture fails). One JSON line per level."""
+    import copy
+    import unet_block as UB
+    for lv in UB.LEVELS:
+        blk = UB.build(lv, dev)
+        x, ctx = UB.inputs(lv, dev)
+        with torch.no_grad():
+            qb = UB.to_int8(copy.deepcopy(blk), dev)
+            cb = torch.compile(blk)
+            t0 = time.perf_counter()
+            cb(x, ctx)
+            torch.cuda.synchronize()
+            compile_s = time.perf_counter() - t0
+            log(f"unet block {lv.name}: compiled in {compile_s:.0f} s")
+            ref, out_c = blk(x, ctx) - x, cb(x, ctx) - x
+            row = {"kind": "unet_block_compiled", "shape": lv.name, "dtype": "float16",
+                   "compile_s": round(compile_s, 1)}
+            for name, fn in (("fp16_eager", lambda: blk(x, ctx)), ("fp16_compiled", lambda: cb(x, ctx)),
+                             ("int8", lambda: qb(x, ctx))):
+                row[f"{name}_ms"] = round(per_call_ms(fn), 4)
+                try:
+                    row[f"{name}_graph_ms"] = round(graph_call_ms(fn, reps=5), 4)
+                except RuntimeError as e:
+                    print(f"[bench] unet block {lv.name} {name}: graph capture failed: {e}", file=sys.stderr,
+                          flush=True)
+                    row[f"{name}_graph_ms"] = None
+            row["compiled_vs_eager"] = _cmp(out_c, ref)
+        print(json.dumps(row), flush=True)
+        del blk, qb, cb, x, ctx
+        torch._dynamo.reset()
+
+
 GEMM_AB_SHAPES = [
     # FLUX's W8A8 linears: name, M, K, N (bf16 activations and output, bias, ConvRot 256)
     ("flux_img_qkv", 4096, 3072, 9216),
@@ -806,6 +843,9 @@ def main():
     ap.add_argument("--gemm-ab", action="store_true",
                     help="only print the same-process GEMM A/B against torch._int_mm (hipBLASLt) at FLUX's "
                          "linear shapes and exit")
+    ap.add_argument("--unet-compiled", action="store_true",
+                    help="only time the UNet transformer block fp16 eager, fp16 under torch.compile and W8A8 + "
+                         "INT8 at SD1.5 / SDXL shapes and exit")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only measure the MFMA-only throughput of the device (int8 and bf16, 1 and 2 waves per "
                          "SIMD, constant and changing operands) and exit")
@@ -832,6 +872,12 @@ def main():
     if args.mfma_ceiling:
         torch.cuda.set_device(0)
         print(json.dumps({"mfma_ceiling": mfma_ceiling()}), flush=True)
+        return
+    if args.unet_compiled:
+        from diffucore_amd import _lib
+        _lib.require()
+        torch.cuda.set_device(0)
+        unet_compiled(torch.device("cuda", 0))
         return
     if args.shapes or args.gemm_ab:
         from diffucore_amd import _lib
