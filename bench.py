@@ -619,6 +619,29 @@ def _cmp(y, ref):
             "cos": float(a @ b / (a.norm() * b.norm()))}
 
 
+def attn_calls(dev, calls: int = 5):
+    """``calls`` INT8 attention calls at each benchmark config self-attention
+    shape (the shapes report's tensors, no graphs, no timing): a short driver
+    for rocprofv3 counter runs."""
+    from diffucore_amd import attention_bhld
+    from diffucore_amd._attention import SHORT_KEYS
+    g = torch.Generator(device=dev)
+    for name, B, H, S, Skv, D, dt, koff in ATTN_SHAPES:
+        if Skv <= SHORT_KEYS:
+            continue
+        g.manual_seed(0)
+        q = torch.randn(B, S, H * D, generator=g, device=dev).to(dt).view(B, S, H, D).transpose(1, 2)
+        k = torch.randn(B, Skv, H, D, generator=g, device=dev)
+        if koff:
+            k = k + torch.randn(H, D, generator=g, device=dev) * koff
+        k = k.to(dt).reshape(B, Skv, H * D).view(B, Skv, H, D).transpose(1, 2)
+        v = torch.randn(B, Skv, H * D, generator=g, device=dev).to(dt).view(B, Skv, H, D).transpose(1, 2)
+        for _ in range(calls):
+            attention_bhld(q, k, v, "int8_turing")
+        torch.cuda.synchronize()
+        log(f"attention {name}: {calls} calls")
+
+
 def shapes_report(dev):
     """One JSON line per benchmark config shape: time, TOPS, % of peak, accuracy."""
     import torch.nn.functional as F
@@ -843,6 +866,9 @@ def main():
     ap.add_argument("--gemm-ab", action="store_true",
                     help="only print the same-process GEMM A/B against torch._int_mm (hipBLASLt) at FLUX's "
                          "linear shapes and exit")
+    ap.add_argument("--attn-calls", action="store_true",
+                    help="only make 5 INT8 attention calls at each benchmark config self-attention shape and exit "
+                         "(a driver for rocprofv3 counter runs)")
     ap.add_argument("--unet-compiled", action="store_true",
                     help="only time the UNet transformer block fp16 eager, fp16 under torch.compile and W8A8 + "
                          "INT8 at SD1.5 / SDXL shapes and exit")
@@ -872,6 +898,13 @@ def main():
     if args.mfma_ceiling:
         torch.cuda.set_device(0)
         print(json.dumps({"mfma_ceiling": mfma_ceiling()}), flush=True)
+        return
+    if args.attn_calls:
+        from diffucore_amd import _lib
+        _lib.require()
+        torch.cuda.set_device(0)
+        with torch.no_grad():
+            attn_calls(torch.device("cuda", 0))
         return
     if args.unet_compiled:
         from diffucore_amd import _lib
